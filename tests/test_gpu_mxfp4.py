@@ -1,0 +1,120 @@
+"""fused_moe_mxfp4 on the GPU against the oracle (mxfp4_reference.py:28-112).
+
+Tolerance 2e-2 / 2e-2 (bf16). Follows the reference's tests/test_moe_mxfp4.py:
+with and without bias and routing weight, swiglu_limit disabled, EP partials,
+fp32 activations, plus the BASELINE config C4 (E=256, hidden=4096, ispp=512,
+top_k=6, M=48) at full size and an exactness probe of the e2m1 decode.
+"""
+from __future__ import annotations
+
+import pytest
+import torch
+
+from oracle import c_oracle
+from oracle.torch_ref import moe_mxfp4_ref
+from tests._helpers import assert_close, softmax_weights, uniform_topk
+from xkernels_amd import Backend, MoeMxfp4Workspace, fused_moe_mxfp4, make_mxfp4_moe_weights
+
+pytestmark = pytest.mark.gpu
+KEYS = ("w13", "w13_scale", "w2", "w2_scale")
+
+
+def _case(M, E, hidden, ispp, top_k, bias=False, dtype=torch.bfloat16, seed=0, **wkw):
+    wts = make_mxfp4_moe_weights(E, hidden, ispp, with_bias=bias, device="cpu", seed=seed, **wkw)
+    g = torch.Generator().manual_seed(seed + 1)
+    A = torch.randn(M, hidden, generator=g).to(dtype)
+    ids = uniform_topk(M, top_k, E, seed + 2)
+    w = softmax_weights(M, top_k, seed + 3)
+    return A, wts, ids, w
+
+
+def _run(A, wts, ids, w, dev, **kw):
+    d = lambda t: None if t is None else t.to(dev)  # noqa: E731
+    return fused_moe_mxfp4(d(A), *(d(wts[k]) for k in KEYS), d(ids), d(w), b13=d(wts["b13"]),
+                           b2=d(wts["b2"]), backend=Backend.HIP, **kw)
+
+
+def _ref(A, wts, ids, w, **kw):
+    return moe_mxfp4_ref(A, *(wts[k] for k in KEYS), ids, w, b13=wts["b13"], b2=wts["b2"], **kw)
+
+
+@pytest.mark.parametrize("M,E,hidden,ispp,top_k", [(4, 8, 256, 64, 2), (1, 16, 512, 128, 6),
+                                                   (7, 8, 256, 96, 3), (48, 32, 512, 64, 6),
+                                                   (40, 4, 128, 32, 2)])
+@pytest.mark.parametrize("bias", [False, True])
+@pytest.mark.parametrize("mul_routed", [True, False])
+def test_matches_oracle(M, E, hidden, ispp, top_k, bias, mul_routed, dev):
+    A, wts, ids, w = _case(M, E, hidden, ispp, top_k, bias=bias)
+    got = _run(A, wts, ids, w, dev, mul_routed_weight=mul_routed)
+    assert got.dtype == torch.bfloat16 and got.shape == (M, hidden)
+    assert_close(got, _ref(A, wts, ids, w, mul_routed_weight=mul_routed), 2e-2, 2e-2, "mxfp4")
+
+
+@pytest.mark.parametrize("limit", [None, 0.0, 1.5])
+def test_swiglu_limit(limit, dev):
+    A, wts, ids, w = _case(6, 8, 256, 64, 2, seed=4)
+    got = _run(A, wts, ids, w, dev, swiglu_limit=limit)
+    assert_close(got, _ref(A, wts, ids, w, swiglu_limit=limit), 2e-2, 2e-2, f"limit={limit}")
+
+
+def test_fp32_activations(dev):
+    A, wts, ids, w = _case(5, 8, 256, 64, 2, dtype=torch.float32, seed=5)
+    got = _run(A, wts, ids, w, dev)
+    assert got.dtype == torch.float32
+    assert_close(got, _ref(A, wts, ids, w), 2e-2, 2e-2, "fp32 A")
+
+
+def test_full_scale_range_and_special_codes(dev):
+    """Scale bytes across [1, 254] plus 0xFF (reads as 0)."""
+    A, wts, ids, w = _case(6, 4, 256, 64, 2, seed=6, scale_lo=110, scale_hi=135)
+    wts["w2_scale"][0, :3, 0] = 255
+    wts["w13_scale"][1, 5, 2] = 255
+    got = _run(A, wts, ids, w, dev)
+    assert_close(got, _ref(A, wts, ids, w), 2e-2, 2e-2, "scale range")
+
+
+def test_decode_is_exact_single_slot(dev):
+    """One token, one expert, weight 1, no clamp: out = bf16-exact pipeline of the C oracle."""
+    A, wts, _, _ = _case(1, 2, 128, 32, 1, seed=8)
+    ids = torch.tensor([[1]], dtype=torch.int32)
+    w = torch.ones(1, 1)
+    got = _run(A, wts, ids, w, dev, swiglu_limit=None)
+    want = c_oracle.mxfp4_moe(A, *(wts[k] for k in KEYS), ids, w, swiglu_limit=None)
+    assert_close(got, want, 1e-2, 1e-2, "single slot")
+
+
+@pytest.mark.parametrize("ep_size", [2, 4])
+def test_expert_parallel_partials(ep_size, dev):
+    E, M = 16, 10
+    A, wts, ids, w = _case(M, E, 256, 64, 4, seed=9)
+    dense = _run(A, wts, ids, w, dev).float()
+    per = E // ep_size
+    total = torch.zeros_like(dense)
+    for r in range(ep_size):
+        emap = torch.full((E,), -1, dtype=torch.int32)
+        emap[r * per:(r + 1) * per] = torch.arange(per, dtype=torch.int32)
+        local = {k: (v[r * per:(r + 1) * per] if v is not None else None) for k, v in wts.items()}
+        part = _run(A, local, ids, w, dev, expert_map=emap)
+        assert_close(part, _ref(A, local, ids, w, expert_map=emap), 2e-2, 2e-2, f"EP rank {r}")
+        total += part.float()
+    assert_close(total, dense, 3e-2, 3e-2, "EP sum")
+
+
+def test_workspace(dev):
+    ws = MoeMxfp4Workspace.allocate(16, 2, 8, 16, 64, 256, dtype=torch.bfloat16, device=dev)
+    for M in (16, 3):
+        A, wts, ids, w = _case(M, 8, 256, 64, 2, seed=M)
+        got = _run(A, wts, ids, w, dev, workspace=ws)
+        assert_close(got, _ref(A, wts, ids, w), 2e-2, 2e-2, f"ws M={M}")
+
+
+def test_config4_full_size(dev):
+    """C4: E=256, hidden=4096, ispp=512, top_k=6, M=48; scale exponents in [-8, 0]."""
+    wts = make_mxfp4_moe_weights(256, 4096, 512, device="cuda", seed=40, scale_lo=119, scale_hi=128)
+    g = torch.Generator(device="cuda").manual_seed(41)
+    A = torch.randn(48, 4096, generator=g, device="cuda").to(torch.bfloat16)
+    ids = uniform_topk(48, 6, 256, 42).cuda()
+    w = softmax_weights(48, 6, 43).cuda()
+    got = fused_moe_mxfp4(A, *(wts[k] for k in KEYS), ids, w, backend=Backend.HIP)
+    want = moe_mxfp4_ref(A, *(wts[k] for k in KEYS), ids, w)  # oracle on the device copy
+    assert_close(got, want, 2e-2, 2e-2, "C4")

@@ -1,0 +1,249 @@
+// extern "C" entry points of libxk_moe.so (declared in include/xk_moe.h).
+//
+// Argument checks happen here, before any launch, so a bad shape is reported as
+// XK_ERR_INVALID instead of reaching a kernel. Pipelines carve their scratch
+// from the caller's workspace; nothing is allocated here.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include <algorithm>
+
+#include "common.h"
+
+namespace xk {
+
+namespace {
+thread_local char g_err[512] = "";
+}
+
+int set_error(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+void clear_error() { g_err[0] = '\0'; }
+
+// kernels (align.hip, reduce.hip, int4_gemm.hip, mxfp4_gemm.hip)
+int64_t align_workspace_bytes(int64_t numel, int num_experts);
+int launch_align(const int32_t* ids, int64_t numel, int num_experts, int block_size,
+                 const int32_t* emap, int num_global, int32_t* sorted_ids, int32_t* expert_ids,
+                 int32_t* num_post, int32_t* expert_offsets, void* workspace,
+                 int64_t workspace_bytes, hipStream_t stream);
+int launch_sum_reduce(const void* y, int y_dtype, int64_t M, int64_t top_k, int64_t H,
+                      const void* w, int w_dtype, float scale, void* out, hipStream_t stream);
+int launch_topk_combine(const float* slot_out, int64_t M, int64_t top_k, int64_t N,
+                        const float* topk_w, int mul_routed_weight, const int32_t* topk_ids,
+                        int num_local, const int32_t* emap, int num_global, void* out,
+                        int out_dtype, hipStream_t stream);
+int int4_block_size();
+bool int4_use_stream(int a_dtype, int group_size, int64_t K);
+int launch_int4_gemm(const void* A, int a_dtype, int64_t M, int64_t K, const int32_t* packed,
+                     const uint16_t* scale, int64_t E, int64_t N, int group_size,
+                     const int32_t* topk_ids, int64_t top_k, const int32_t* emap,
+                     int num_global, const int32_t* sorted_ids, const int32_t* offsets,
+                     float* slot_out, hipStream_t stream);
+int mxfp4_block_size();
+int launch_mxfp4_stage(int stage, const void* A, int a_dtype, const uint8_t* w,
+                       const uint8_t* ws, const uint16_t* bias, int64_t E, int64_t K,
+                       int64_t rows, int64_t ncols, const int32_t* sorted_ids,
+                       const int32_t* offsets, int64_t numel, int64_t top_k, float limit,
+                       uint16_t* act, float* slot_out, hipStream_t stream);
+
+namespace {
+
+constexpr int64_t kAlign = 256;
+int64_t round_up(int64_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
+
+// Scratch of one align call: the outputs the GEMMs consume plus the align's own
+// grid scratch.
+struct AlignScratch {
+  int64_t sorted, expert_ids, num_post, offsets, inner, total;
+  AlignScratch(int64_t numel, int num_experts, int block_size) {
+    const int64_t max_pad = numel + int64_t(num_experts + 1) * (block_size - 1);
+    const int64_t max_blocks = cdiv(max_pad, block_size);
+    int64_t o = 0;
+    sorted = o; o += round_up(max_pad * 4);
+    expert_ids = o; o += round_up(max_blocks * 4);
+    num_post = o; o += round_up(4);
+    offsets = o; o += round_up(int64_t(num_experts + 1) * 4);
+    inner = o; o += round_up(align_workspace_bytes(numel, num_experts));
+    total = o;
+  }
+};
+
+template <typename T> T* at(void* base, int64_t off) {
+  return reinterpret_cast<T*>(static_cast<char*>(base) + off);
+}
+
+int check_dtype(int dt, const char* what) {
+  if (dt != XK_DT_BF16 && dt != XK_DT_FP32)
+    return set_error(XK_ERR_INVALID, "%s: dtype code %d is neither bf16 nor fp32", what, dt);
+  return XK_OK;
+}
+
+}  // namespace
+}  // namespace xk
+
+using namespace xk;
+
+extern "C" {
+
+const char* xk_last_error(void) { return g_err; }
+
+int xk_abi_version(void) { return 100; }
+
+int64_t xk_moe_align_workspace_bytes(int64_t numel, int32_t num_experts) {
+  return align_workspace_bytes(numel, num_experts);
+}
+
+int xk_moe_align_block_size(const int32_t* topk_ids, int64_t numel, int32_t num_experts,
+                            int32_t block_size, const int32_t* expert_map,
+                            int32_t num_global_experts, int32_t* sorted_token_ids,
+                            int32_t* expert_ids, int32_t* num_tokens_post_padded,
+                            int32_t* expert_offsets, void* workspace, int64_t workspace_bytes,
+                            hipStream_t stream) {
+  clear_error();
+  return launch_align(topk_ids, numel, num_experts, block_size, expert_map, num_global_experts,
+                      sorted_token_ids, expert_ids, num_tokens_post_padded, expert_offsets,
+                      workspace, workspace_bytes, stream);
+}
+
+int xk_moe_sum_reduce(const void* y, int32_t y_dtype, int64_t M, int64_t top_k, int64_t H,
+                      const void* w, int32_t w_dtype, float routed_scaling_factor, void* out,
+                      hipStream_t stream) {
+  clear_error();
+  return launch_sum_reduce(y, y_dtype, M, top_k, H, w, w_dtype, routed_scaling_factor, out,
+                           stream);
+}
+
+int32_t xk_moe_int4_block_size(int64_t M, int64_t top_k, int64_t E) {
+  (void)M; (void)top_k; (void)E;
+  return int4_block_size();
+}
+
+int64_t xk_moe_int4_w4a16_workspace_bytes(int64_t M, int64_t top_k, int64_t E, int64_t N,
+                                          int64_t K) {
+  (void)K;
+  const int64_t numel = M * top_k;
+  AlignScratch al(numel, int(E), int4_block_size());
+  return al.total + round_up(numel * N * 4);
+}
+
+int xk_moe_int4_w4a16_gemm(const void* A, int32_t a_dtype, int64_t M, int64_t K,
+                           const int32_t* packed, const uint16_t* scale, int64_t E, int64_t N,
+                           int32_t group_size, const int32_t* topk_ids, int64_t top_k,
+                           const int32_t* expert_map, int32_t num_global_experts,
+                           const int32_t* sorted_token_ids, const int32_t* expert_offsets,
+                           float* slot_out, hipStream_t stream) {
+  clear_error();
+  return launch_int4_gemm(A, a_dtype, M, K, packed, scale, E, N, group_size, topk_ids, top_k,
+                          expert_map, num_global_experts, sorted_token_ids, expert_offsets,
+                          slot_out, stream);
+}
+
+int xk_moe_topk_combine(const float* slot_out, int64_t M, int64_t top_k, int64_t N,
+                        const float* topk_w, int32_t mul_routed_weight,
+                        const int32_t* topk_ids, int32_t num_local_experts,
+                        const int32_t* expert_map, int32_t num_global_experts, void* out,
+                        int32_t out_dtype, hipStream_t stream) {
+  clear_error();
+  return launch_topk_combine(slot_out, M, top_k, N, topk_w, mul_routed_weight, topk_ids,
+                             num_local_experts, expert_map, num_global_experts, out, out_dtype,
+                             stream);
+}
+
+int xk_moe_int4_w4a16(const void* A, int32_t a_dtype, int64_t M, int64_t K,
+                      const int32_t* packed, const uint16_t* scale, int64_t E, int64_t N,
+                      int32_t group_size, const int32_t* topk_ids, const float* topk_w,
+                      int64_t top_k, const int32_t* expert_map, int32_t num_global_experts,
+                      int32_t mul_routed_weight, void* out, void* workspace,
+                      int64_t workspace_bytes, hipStream_t stream) {
+  clear_error();
+  if (int rc = check_dtype(a_dtype, "int4 A")) return rc;
+  XK_REQUIRE(M >= 0 && top_k >= 1 && E >= 1 && N >= 1, "int4: bad sizes M=%lld top_k=%lld E=%lld N=%lld",
+             (long long)M, (long long)top_k, (long long)E, (long long)N);
+  XK_REQUIRE(out != nullptr || M == 0, "int4: null out");
+  XK_REQUIRE(M == 0 || (A && packed && scale && topk_ids), "int4: null input pointer");
+  XK_REQUIRE(!mul_routed_weight || topk_w || M == 0, "int4: null topk_w");
+  if (M == 0) return XK_OK;
+  const int64_t need = xk_moe_int4_w4a16_workspace_bytes(M, top_k, E, N, K);
+  if (workspace == nullptr || workspace_bytes < need)
+    return set_error(XK_ERR_WORKSPACE, "int4: workspace %lld B < %lld B",
+                     (long long)workspace_bytes, (long long)need);
+  const int64_t numel = M * top_k;
+  AlignScratch al(numel, int(E), int4_block_size());
+  float* slot_out = at<float>(workspace, al.total);
+  const int32_t* sorted = nullptr;
+  const int32_t* offsets = nullptr;
+  if (int4_use_stream(a_dtype, group_size, K)) {
+    int rc = launch_align(topk_ids, numel, int(E), int4_block_size(), expert_map,
+                          num_global_experts, at<int32_t>(workspace, al.sorted),
+                          at<int32_t>(workspace, al.expert_ids),
+                          at<int32_t>(workspace, al.num_post),
+                          at<int32_t>(workspace, al.offsets), at<char>(workspace, al.inner),
+                          al.total - al.inner, stream);
+    if (rc) return rc;
+    sorted = at<int32_t>(workspace, al.sorted);
+    offsets = at<int32_t>(workspace, al.offsets);
+  }
+  if (int rc = launch_int4_gemm(A, a_dtype, M, K, packed, scale, E, N, group_size, topk_ids,
+                                top_k, expert_map, num_global_experts, sorted, offsets,
+                                slot_out, stream))
+    return rc;
+  return launch_topk_combine(slot_out, M, top_k, N, topk_w, mul_routed_weight, topk_ids,
+                             int(E), expert_map, num_global_experts, out, a_dtype, stream);
+}
+
+int64_t xk_moe_mxfp4_workspace_bytes(int64_t M, int64_t top_k, int64_t E, int64_t hidden,
+                                     int64_t ispp) {
+  const int64_t numel = M * top_k;
+  AlignScratch al(numel, int(E), mxfp4_block_size());
+  return al.total + round_up(numel * ispp * 2) + round_up(numel * hidden * 4);
+}
+
+int xk_moe_mxfp4(const void* A, int32_t a_dtype, int64_t M, int64_t hidden, const uint8_t* w13,
+                 const uint8_t* w13_scale, const uint8_t* w2, const uint8_t* w2_scale,
+                 int64_t E, int64_t ispp, const uint16_t* b13, const uint16_t* b2,
+                 float swiglu_limit, int32_t group_size, const int32_t* topk_ids,
+                 const float* topk_w, int64_t top_k, const int32_t* expert_map,
+                 int32_t num_global_experts, int32_t mul_routed_weight, void* out,
+                 void* workspace, int64_t workspace_bytes, hipStream_t stream) {
+  clear_error();
+  if (int rc = check_dtype(a_dtype, "mxfp4 A")) return rc;
+  XK_REQUIRE(group_size == 32, "mxfp4: group_size=%d (only the OCP MX block of 32)", group_size);
+  XK_REQUIRE(M >= 0 && top_k >= 1 && E >= 1 && hidden >= 32 && ispp >= 32,
+             "mxfp4: bad sizes M=%lld top_k=%lld E=%lld hidden=%lld ispp=%lld", (long long)M,
+             (long long)top_k, (long long)E, (long long)hidden, (long long)ispp);
+  XK_REQUIRE(hidden % 32 == 0 && ispp % 32 == 0, "mxfp4: hidden and ispp must be multiples of 32");
+  XK_REQUIRE(M == 0 || (A && w13 && w13_scale && w2 && w2_scale && topk_ids && out),
+             "mxfp4: null pointer");
+  XK_REQUIRE(!mul_routed_weight || topk_w || M == 0, "mxfp4: null topk_w");
+  if (M == 0) return XK_OK;
+  const int64_t need = xk_moe_mxfp4_workspace_bytes(M, top_k, E, hidden, ispp);
+  if (workspace == nullptr || workspace_bytes < need)
+    return set_error(XK_ERR_WORKSPACE, "mxfp4: workspace %lld B < %lld B",
+                     (long long)workspace_bytes, (long long)need);
+  const int64_t numel = M * top_k;
+  AlignScratch al(numel, int(E), mxfp4_block_size());
+  uint16_t* act = at<uint16_t>(workspace, al.total);
+  float* slot_out = at<float>(workspace, al.total + round_up(numel * ispp * 2));
+  int32_t* sorted = at<int32_t>(workspace, al.sorted);
+  int32_t* offsets = at<int32_t>(workspace, al.offsets);
+  int rc = launch_align(topk_ids, numel, int(E), mxfp4_block_size(), expert_map,
+                        num_global_experts, sorted, at<int32_t>(workspace, al.expert_ids),
+                        at<int32_t>(workspace, al.num_post), offsets,
+                        at<char>(workspace, al.inner), al.total - al.inner, stream);
+  if (rc) return rc;
+  rc = launch_mxfp4_stage(0, A, a_dtype, w13, w13_scale, b13, E, hidden, 2 * ispp, ispp, sorted,
+                          offsets, numel, top_k, swiglu_limit, act, nullptr, stream);
+  if (rc) return rc;
+  rc = launch_mxfp4_stage(1, act, XK_DT_BF16, w2, w2_scale, b2, E, ispp, hidden, hidden, sorted,
+                          offsets, numel, top_k, 0.f, nullptr, slot_out, stream);
+  if (rc) return rc;
+  return launch_topk_combine(slot_out, M, top_k, hidden, topk_w, mul_routed_weight, topk_ids,
+                             int(E), expert_map, num_global_experts, out, a_dtype, stream);
+}
+
+}  // extern "C"

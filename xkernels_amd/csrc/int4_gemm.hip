@@ -1,0 +1,322 @@
+// Grouped INT4 W4A16 MoE GEMM for gfx950 (the reference's _fused_moe_int4_kernel,
+// src/xkernels/ops/moe/triton/moe_int4_kernel.py:78-272; math of the oracle
+// reference.py:22-70 with the dequant of w4a16.py:21-50).
+//
+// For every routed slot t (token m = t / top_k, local expert e) this writes the
+// un-weighted fp32 row   slot_out[t, n] = sum_k A[m, k] * W[e, n, k]
+// with W[e, n, k] = (nibble(e, n, k) - 8) * scale[e, n, k / 32]. The weighted
+// top-k combine runs afterwards (reduce.hip).
+//
+// Stream kernel (bf16 A, group 32) — the decode regime is weight-streaming
+// bound, so every packed weight byte is read from HBM exactly once:
+//   * one workgroup owns (expert e, 128 output columns) and ALL of e's slots,
+//     taking them 32 at a time, so an expert's weights are streamed once per
+//     32 routed slots (decode experts hold ~11);
+//   * wave w owns 32 columns = two 16x16 MFMA column tiles; lane (c, q) reads
+//     word q of every 32-k group of its column with a 4-byte load, so one
+//     v_mfma_f32_16x16x32_bf16 contracts exactly one quantisation group;
+//   * nibbles become bf16 (128 + n) with one v_and_or_b32 per two values (the
+//     exponent of 128 places the nibble in the mantissa); the MFMA then gives
+//     D = sum a*(128+n) and the group result is s * (D - 136 * sum(a)), where
+//     sum(a) over the 32 activations of the group is computed once per
+//     workgroup while staging A into LDS. The dequantised weight (n-8)*s is
+//     exact in fp32 this way; the reference rounds it to bf16 first, a
+//     difference far inside the op's 2e-2 tolerance;
+//   * A (the expert's activation rows, 32 x 256 k per chunk) is staged in LDS
+//     with the same k-permutation the nibble unpack produces, and the next
+//     chunk's weights, scales and activations are prefetched into registers
+//     while the current chunk is contracted.
+// Simple kernel: any dtype / group size, one thread per (slot, column), exact
+// dequant rounded to A's dtype like the reference. Correctness fallback for the
+// fp32 sweep points and unusual group sizes.
+#include "common.h"
+
+namespace xk {
+namespace {
+
+constexpr int kWaves = 4;
+constexpr int kColsPerWave = 32;
+constexpr int kColsPerWG = kWaves * kColsPerWave;  // 128
+constexpr int kChunkGroups = 8;                    // 8 x 32 k = 256 k per chunk
+constexpr int kChunkK = kChunkGroups * 32;
+constexpr int kRowsPerPass = 32;                   // two 16-row MFMA tiles
+constexpr int kALdsStride = kChunkK + 8;           // bf16 elements, +16 B pad
+
+struct StreamArgs {
+  const uint16_t* A;       // [M, K] bf16
+  const uint32_t* packed;  // [E, N, K/8]
+  const uint16_t* scale;   // [E, N, K/32] bf16
+  const int32_t* sorted_ids;
+  const int32_t* offsets;  // [E+1] padded prefix (slots), multiples of 16
+  float* out;              // [numel, N]
+  int K, N, numel, top_k;
+  int scale_vec;           // scale rows are 16-byte aligned (K/32 % 8 == 0)
+};
+
+__device__ __forceinline__ uint32_t nib_pair(uint32_t w, int shift) {
+  // bf16 pair (128 + nibble[d], 128 + nibble[d+4]) for d = shift / 4
+  return ((w >> shift) & 0x000F000Fu) | 0x43004300u;
+}
+
+// Reorders 8 consecutive bf16 (4 dwords a0a1 a2a3 a4a5 a6a7) into the order
+// the nibble unpack yields: a0a4 a1a5 a2a6 a3a7.
+__device__ __forceinline__ void perm8(const uint32_t* in, uint32_t* o) {
+  o[0] = (in[0] & 0xFFFFu) | (in[2] << 16);
+  o[1] = (in[0] >> 16) | (in[2] & 0xFFFF0000u);
+  o[2] = (in[1] & 0xFFFFu) | (in[3] << 16);
+  o[3] = (in[1] >> 16) | (in[3] & 0xFFFF0000u);
+}
+
+__global__ void __launch_bounds__(256)
+int4_stream_gemm(StreamArgs p) {
+  __shared__ __attribute__((aligned(16))) uint16_t a_lds[kRowsPerPass * kALdsStride];
+  __shared__ __attribute__((aligned(16))) float r_lds[kChunkGroups * kRowsPerPass];
+  __shared__ int slot_lds[kRowsPerPass];
+  __shared__ int tok_lds[kRowsPerPass];
+
+  const int e = blockIdx.y;
+  const int beg = p.offsets[e], end = p.offsets[e + 1];
+  if (beg >= end) return;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int c16 = lane & 15, q = lane >> 4;
+  const int K = p.K, N = p.N, G = K >> 5, KW = K >> 3;
+  const int n_base = blockIdx.x * kColsPerWG + wave * kColsPerWave;
+
+  const uint32_t* wrow[2];
+  const uint16_t* srow[2];
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    const int n = min(n_base + 16 * c + c16, N - 1);
+    wrow[c] = p.packed + (static_cast<int64_t>(e) * N + n) * KW + q;
+    srow[c] = p.scale + (static_cast<int64_t>(e) * N + n) * G;
+  }
+  // Staging role: thread -> (row r, group gg) of the 32 x 8 activation chunk.
+  const int st_r = tid >> 3, st_g = tid & 7;
+
+  for (int pass = beg; pass < end; pass += kRowsPerPass) {
+    const int ntiles = min(2, (end - pass) >> 4);
+    __syncthreads();  // previous pass finished with slot_lds / tok_lds
+    if (tid < kRowsPerPass) {
+      int slot = -1, tok = -1;
+      if (tid < ntiles * 16) {
+        const int s = p.sorted_ids[pass + tid];
+        if (s < p.numel) { slot = s; tok = s / p.top_k; }
+      }
+      slot_lds[tid] = slot;
+      tok_lds[tid] = tok;
+    }
+    __syncthreads();
+    const int my_tok = tok_lds[st_r];
+
+    auto load_a = [&](int g0, uint32_t* areg) {
+      const int g = g0 + st_g;
+      if (my_tok >= 0 && g < G) {
+        const u32x4* src = reinterpret_cast<const u32x4*>(
+            p.A + static_cast<int64_t>(my_tok) * K + g * 32);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const u32x4 v = src[j];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) areg[4 * j + i] = v[i];
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) areg[i] = 0u;
+      }
+    };
+    auto load_w = [&](int g0, uint32_t (*wreg)[kChunkGroups], uint32_t (*sreg)[4]) {
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+#pragma unroll
+        for (int g = 0; g < kChunkGroups; ++g)
+          wreg[c][g] = (g0 + g < G) ? wrow[c][(g0 + g) * 4] : 0u;
+        if (p.scale_vec) {
+          const u32x4 s4 = *reinterpret_cast<const u32x4*>(srow[c] + g0);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) sreg[c][i] = s4[i];
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const uint32_t lo = (g0 + 2 * i < G) ? srow[c][g0 + 2 * i] : 0u;
+            const uint32_t hi = (g0 + 2 * i + 1 < G) ? srow[c][g0 + 2 * i + 1] : 0u;
+            sreg[c][i] = lo | (hi << 16);
+          }
+        }
+      }
+    };
+
+    f32x4 acc[2][2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int c = 0; c < 2; ++c) acc[t][c] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    uint32_t areg[16];
+    uint32_t wcur[2][kChunkGroups], wnext[2][kChunkGroups];
+    uint32_t scur[2][4], snext[2][4];
+    load_a(0, areg);
+    load_w(0, wcur, scur);
+
+    for (int g0 = 0; g0 < G; g0 += kChunkGroups) {
+      __syncthreads();  // all waves done reading the previous chunk
+      {
+        // write staged activations (k-permuted) and their group sums
+        float rs = 0.f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          rs += __uint_as_float(areg[i] << 16) + __uint_as_float(areg[i] & 0xFFFF0000u);
+        uint32_t o[16];
+#pragma unroll
+        for (int s = 0; s < 4; ++s) perm8(areg + 4 * s, o + 4 * s);
+        u32x4* dst = reinterpret_cast<u32x4*>(a_lds + st_r * kALdsStride + st_g * 32);
+#pragma unroll
+        for (int s = 0; s < 4; ++s) dst[s] = u32x4{o[4 * s], o[4 * s + 1], o[4 * s + 2], o[4 * s + 3]};
+        r_lds[st_g * kRowsPerPass + st_r] = rs;
+      }
+      __syncthreads();
+      const int gn = g0 + kChunkGroups;
+      if (gn < G) {
+        load_a(gn, areg);
+        load_w(gn, wnext, snext);
+      }
+#pragma unroll
+      for (int g = 0; g < kChunkGroups; ++g) {
+        if (g0 + g >= G) break;
+        bf16x8 bfrag[2];
+        float sc[2];
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+          const uint32_t w = wcur[c][g];
+          const u32x4 b = u32x4{nib_pair(w, 0), nib_pair(w, 4), nib_pair(w, 8), nib_pair(w, 12)};
+          bfrag[c] = __builtin_bit_cast(bf16x8, b);
+          const uint32_t sw = scur[c][g >> 1];
+          sc[c] = __uint_as_float((g & 1) ? (sw & 0xFFFF0000u) : (sw << 16));
+        }
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          if (t >= ntiles) break;
+          const bf16x8 afrag = *reinterpret_cast<const bf16x8*>(
+              a_lds + (t * 16 + c16) * kALdsStride + g * 32 + q * 8);
+          const f32x4 r4 = *reinterpret_cast<const f32x4*>(r_lds + g * kRowsPerPass + t * 16 + q * 4);
+#pragma unroll
+          for (int c = 0; c < 2; ++c) {
+            const f32x4 d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                afrag, bfrag[c], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              acc[t][c][i] = fmaf(sc[c], fmaf(-136.0f, r4[i], d[i]), acc[t][c][i]);
+          }
+        }
+      }
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+#pragma unroll
+        for (int g = 0; g < kChunkGroups; ++g) wcur[c][g] = wnext[c][g];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) scur[c][i] = snext[c][i];
+      }
+    }
+
+    // epilogue: D row (4q + i) of tile t, column c16 of column tile c
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      if (t >= ntiles) break;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int slot = slot_lds[t * 16 + q * 4 + i];
+        if (slot < 0) continue;
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+          const int n = n_base + 16 * c + c16;
+          if (n < N) p.out[static_cast<int64_t>(slot) * N + n] = acc[t][c][i];
+        }
+      }
+    }
+  }
+}
+
+// One thread per (slot, column); exact dequant rounded to A's dtype.
+template <typename TA>
+__global__ void __launch_bounds__(256)
+int4_simple_gemm(const TA* __restrict__ A, int K, const uint32_t* __restrict__ packed,
+                 const uint16_t* __restrict__ scale, int N, int group_size,
+                 const int32_t* __restrict__ ids, const int32_t* __restrict__ emap,
+                 int num_global, int num_local, int numel, int top_k,
+                 float* __restrict__ out) {
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (idx >= static_cast<int64_t>(numel) * N) return;
+  const int t = static_cast<int>(idx / N), n = static_cast<int>(idx - static_cast<int64_t>(t) * N);
+  const int e = map_expert(ids[t], emap, num_global, num_local);
+  if (e < 0) return;
+  const int m = t / top_k;
+  const int G = K / group_size;
+  const uint32_t* wr = packed + (static_cast<int64_t>(e) * N + n) * (K >> 3);
+  const uint16_t* sr = scale + (static_cast<int64_t>(e) * N + n) * G;
+  const TA* ar = A + static_cast<int64_t>(m) * K;
+  float acc = 0.f;
+  for (int kw = 0; kw < (K >> 3); ++kw) {
+    const uint32_t w = wr[kw];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int k = kw * 8 + j;
+      const float s = bf16_to_f32(sr[k / group_size]);
+      float v = static_cast<float>(static_cast<int>((w >> (4 * j)) & 0xFu) - 8) * s;
+      if (sizeof(TA) == 2) v = round_bf16(v);
+      acc = fmaf(io<TA>::load(ar + k), v, acc);
+    }
+  }
+  out[static_cast<int64_t>(t) * N + n] = acc;
+}
+
+}  // namespace
+
+// Token-slot block size the stream kernel consumes (one MFMA row tile).
+int int4_block_size() { return 16; }
+
+bool int4_use_stream(int a_dtype, int group_size, int64_t K) {
+  return a_dtype == XK_DT_BF16 && group_size == 32 && K % 32 == 0 && K >= 32;
+}
+
+int launch_int4_gemm(const void* A, int a_dtype, int64_t M, int64_t K, const int32_t* packed,
+                     const uint16_t* scale, int64_t E, int64_t N, int group_size,
+                     const int32_t* topk_ids, int64_t top_k, const int32_t* emap,
+                     int num_global, const int32_t* sorted_ids, const int32_t* offsets,
+                     float* slot_out, hipStream_t stream) {
+  XK_REQUIRE(a_dtype == XK_DT_BF16 || a_dtype == XK_DT_FP32, "int4: bad A dtype %d", a_dtype);
+  XK_REQUIRE(M >= 0 && top_k >= 1 && E >= 1 && N >= 1 && K >= 8, "int4: bad sizes");
+  XK_REQUIRE(K % 8 == 0, "int4: K=%lld not a multiple of 8", (long long)K);
+  XK_REQUIRE(group_size > 0 && K % group_size == 0, "int4: group_size=%d does not divide K",
+             group_size);
+  XK_REQUIRE(E <= 65535 && N < (int64_t(1) << 30) && K < (int64_t(1) << 30), "int4: size limit");
+  const int64_t numel = M * top_k;
+  XK_REQUIRE(numel < (int64_t(1) << 30), "int4: M*top_k too large");
+  if (numel == 0) return XK_OK;
+  if (int4_use_stream(a_dtype, group_size, K)) {
+    XK_REQUIRE(sorted_ids && offsets, "int4: stream kernel needs align outputs");
+    XK_REQUIRE(reinterpret_cast<uintptr_t>(A) % 16 == 0, "int4: A must be 16-byte aligned");
+    StreamArgs a{static_cast<const uint16_t*>(A), reinterpret_cast<const uint32_t*>(packed),
+                 scale, sorted_ids, offsets, slot_out, int(K), int(N), int(numel), int(top_k),
+                 int((K / 32) % 8 == 0 && reinterpret_cast<uintptr_t>(scale) % 16 == 0)};
+    const dim3 grid(static_cast<unsigned>(cdiv(N, kColsPerWG)), static_cast<unsigned>(E));
+    hipLaunchKernelGGL(int4_stream_gemm, grid, dim3(256), 0, stream, a);
+    XK_CHECK_LAUNCH("int4_stream_gemm");
+    return XK_OK;
+  }
+  const int64_t total = numel * N;
+  const dim3 grid(static_cast<unsigned>(cdiv(total, 256)));
+  if (a_dtype == XK_DT_BF16)
+    hipLaunchKernelGGL((int4_simple_gemm<uint16_t>), grid, dim3(256), 0, stream,
+                       static_cast<const uint16_t*>(A), int(K),
+                       reinterpret_cast<const uint32_t*>(packed), scale, int(N), group_size,
+                       topk_ids, emap, num_global, int(E), int(numel), int(top_k), slot_out);
+  else
+    hipLaunchKernelGGL((int4_simple_gemm<float>), grid, dim3(256), 0, stream,
+                       static_cast<const float*>(A), int(K),
+                       reinterpret_cast<const uint32_t*>(packed), scale, int(N), group_size,
+                       topk_ids, emap, num_global, int(E), int(numel), int(top_k), slot_out);
+  XK_CHECK_LAUNCH("int4_simple_gemm");
+  return XK_OK;
+}
+
+}  // namespace xk

@@ -1,0 +1,189 @@
+// Weighted top-k reduction kernels for gfx950.
+//
+//   moe_sum_reduce  (sum_reduce.py:20-39):
+//     out[m, h] = s * sum_k w[m, k] * y[m, k, h]        fp32 accumulate, y dtype out
+//   top-k combine   (the reduce after the grouped GEMMs; reference.py:59-70,
+//                    mxfp4_reference.py:104-112):
+//     out[m, n] = sum_j valid(m, j) * [w[m, j]] * slot_out[m*top_k + j, n]
+//
+// Pure HBM streaming. One thread owns VEC consecutive elements of one output
+// row and walks the top_k inputs with 16-byte loads (bf16: 8 elements, fp32:
+// 2 x 4), so every load instruction of a wavefront covers 1 KiB contiguous.
+// The k loop is fully unrolled for the common top_k so all loads issue before
+// the first add.
+#include "common.h"
+
+namespace xk {
+namespace {
+
+template <typename T, int VEC> struct vec_io;
+template <> struct vec_io<uint16_t, 8> {
+  __device__ __forceinline__ static void load(const uint16_t* p, float* v) {
+    const u32x4 r = *reinterpret_cast<const u32x4*>(p);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[2 * i] = __uint_as_float(r[i] << 16);
+      v[2 * i + 1] = __uint_as_float(r[i] & 0xFFFF0000u);
+    }
+  }
+  __device__ __forceinline__ static void store(uint16_t* p, const float* v) {
+    u32x4 r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      r[i] = static_cast<uint32_t>(f32_to_bf16(v[2 * i])) |
+             (static_cast<uint32_t>(f32_to_bf16(v[2 * i + 1])) << 16);
+    *reinterpret_cast<u32x4*>(p) = r;
+  }
+};
+template <> struct vec_io<float, 8> {
+  __device__ __forceinline__ static void load(const float* p, float* v) {
+    const f32x4 a = reinterpret_cast<const f32x4*>(p)[0];
+    const f32x4 b = reinterpret_cast<const f32x4*>(p)[1];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) { v[i] = a[i]; v[4 + i] = b[i]; }
+  }
+  __device__ __forceinline__ static void store(float* p, const float* v) {
+    f32x4 a, b;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) { a[i] = v[i]; b[i] = v[4 + i]; }
+    reinterpret_cast<f32x4*>(p)[0] = a;
+    reinterpret_cast<f32x4*>(p)[1] = b;
+  }
+};
+template <typename T> struct vec_io<T, 1> {
+  __device__ __forceinline__ static void load(const T* p, float* v) { v[0] = io<T>::load(p); }
+  __device__ __forceinline__ static void store(T* p, const float* v) { io<T>::store(p, v[0]); }
+};
+
+// Row weights: per (m, k) multiplier applied to y[m, k, :]. Covers the plain
+// sum (no weights), weights in fp32 or bf16, and the combine's validity mask.
+struct RowWeights {
+  const void* w;        // [M, top_k] or null
+  int w_dtype;          // XK_DT_*
+  const int32_t* ids;   // [M, top_k] or null (no mask)
+  const int32_t* emap;  // nullable
+  int num_global, num_local;
+
+  __device__ __forceinline__ float get(int64_t idx) const {
+    if (w == nullptr) return 1.0f;
+    return (w_dtype == XK_DT_FP32) ? static_cast<const float*>(w)[idx]
+                                   : bf16_to_f32(static_cast<const uint16_t*>(w)[idx]);
+  }
+  // Dropped slots are skipped (their rows were never written, so they are
+  // selected away rather than multiplied by zero).
+  __device__ __forceinline__ bool valid(int64_t idx) const {
+    return ids == nullptr || map_expert(ids[idx], emap, num_global, num_local) >= 0;
+  }
+};
+
+template <typename Tin, typename Tout, int VEC, int KFIX>
+__global__ void __launch_bounds__(256)
+topk_reduce(const Tin* __restrict__ y, int64_t M, int top_k_rt, int64_t H, RowWeights rw,
+            float scale, Tout* __restrict__ out) {
+  const int top_k = KFIX > 0 ? KFIX : top_k_rt;
+  const int64_t chunks_per_row = H / VEC;
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (idx >= M * chunks_per_row) return;
+  const int64_t m = idx / chunks_per_row;
+  const int64_t h = (idx - m * chunks_per_row) * VEC;
+  float acc[VEC];
+#pragma unroll
+  for (int i = 0; i < VEC; ++i) acc[i] = 0.0f;
+  const Tin* src = y + (m * top_k) * H + h;
+  if (KFIX > 0) {
+    float v[KFIX > 0 ? KFIX : 1][VEC];
+    float wk[KFIX > 0 ? KFIX : 1];
+    bool ok[KFIX > 0 ? KFIX : 1];
+#pragma unroll
+    for (int k = 0; k < KFIX; ++k) {
+      wk[k] = rw.get(m * top_k + k);
+      ok[k] = rw.valid(m * top_k + k);
+      vec_io<Tin, VEC>::load(src + k * H, v[k]);
+    }
+#pragma unroll
+    for (int k = 0; k < KFIX; ++k)
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) acc[i] += ok[k] ? v[k][i] * wk[k] : 0.0f;
+  } else {
+    for (int k = 0; k < top_k; ++k) {
+      if (!rw.valid(m * top_k + k)) continue;
+      float v[VEC];
+      const float wk = rw.get(m * top_k + k);
+      vec_io<Tin, VEC>::load(src + k * H, v);
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) acc[i] += v[i] * wk;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < VEC; ++i) acc[i] *= scale;
+  vec_io<Tout, VEC>::store(out + m * H + h, acc);
+}
+
+template <typename Tin, typename Tout, int VEC>
+int launch_vec(const Tin* y, int64_t M, int top_k, int64_t H, const RowWeights& rw,
+               float scale, Tout* out, hipStream_t stream) {
+  const int64_t n = M * (H / VEC);
+  if (n == 0) return XK_OK;
+  const dim3 grid(static_cast<unsigned>(cdiv(n, 256))), block(256);
+  switch (top_k) {
+#define XK_K(K)                                                                      \
+  case K:                                                                            \
+    hipLaunchKernelGGL((topk_reduce<Tin, Tout, VEC, K>), grid, block, 0, stream, y, M, \
+                       top_k, H, rw, scale, out);                                    \
+    break;
+    XK_K(1) XK_K(2) XK_K(4) XK_K(6) XK_K(8)
+#undef XK_K
+    default:
+      hipLaunchKernelGGL((topk_reduce<Tin, Tout, VEC, 0>), grid, block, 0, stream, y, M,
+                         top_k, H, rw, scale, out);
+  }
+  XK_CHECK_LAUNCH("topk_reduce");
+  return XK_OK;
+}
+
+template <typename Tin, typename Tout>
+int launch_reduce(const Tin* y, int64_t M, int top_k, int64_t H, const RowWeights& rw,
+                  float scale, Tout* out, hipStream_t stream) {
+  const bool aligned = (reinterpret_cast<uintptr_t>(y) % 16 == 0) &&
+                       (reinterpret_cast<uintptr_t>(out) % 16 == 0);
+  if (H % 8 == 0 && aligned) return launch_vec<Tin, Tout, 8>(y, M, top_k, H, rw, scale, out, stream);
+  return launch_vec<Tin, Tout, 1>(y, M, top_k, H, rw, scale, out, stream);
+}
+
+}  // namespace
+
+int launch_sum_reduce(const void* y, int y_dtype, int64_t M, int64_t top_k, int64_t H,
+                      const void* w, int w_dtype, float scale, void* out,
+                      hipStream_t stream) {
+  XK_REQUIRE(y_dtype == XK_DT_BF16 || y_dtype == XK_DT_FP32, "sum_reduce: bad y dtype %d", y_dtype);
+  XK_REQUIRE(w == nullptr || w_dtype == XK_DT_BF16 || w_dtype == XK_DT_FP32,
+             "sum_reduce: bad w dtype %d", w_dtype);
+  XK_REQUIRE(M >= 0 && top_k >= 0 && H >= 0, "sum_reduce: negative size");
+  XK_REQUIRE(top_k <= 1024, "sum_reduce: top_k=%lld > 1024", (long long)top_k);
+  XK_REQUIRE(M * H == 0 || (y && out), "sum_reduce: null pointer");
+  const RowWeights rw{w, w_dtype, nullptr, nullptr, 0, 0};
+  if (y_dtype == XK_DT_BF16)
+    return launch_reduce(static_cast<const uint16_t*>(y), M, int(top_k), H, rw, scale,
+                         static_cast<uint16_t*>(out), stream);
+  return launch_reduce(static_cast<const float*>(y), M, int(top_k), H, rw, scale,
+                       static_cast<float*>(out), stream);
+}
+
+int launch_topk_combine(const float* slot_out, int64_t M, int64_t top_k, int64_t N,
+                        const float* topk_w, int mul_routed_weight, const int32_t* topk_ids,
+                        int num_local, const int32_t* emap, int num_global, void* out,
+                        int out_dtype, hipStream_t stream) {
+  XK_REQUIRE(out_dtype == XK_DT_BF16 || out_dtype == XK_DT_FP32, "combine: bad out dtype %d",
+             out_dtype);
+  XK_REQUIRE(!mul_routed_weight || topk_w, "combine: null topk_w");
+  XK_REQUIRE(top_k >= 1 && top_k <= 1024, "combine: top_k=%lld outside [1, 1024]",
+             (long long)top_k);
+  const RowWeights rw{mul_routed_weight ? topk_w : nullptr, XK_DT_FP32, topk_ids, emap,
+                      num_global, num_local};
+  if (out_dtype == XK_DT_BF16)
+    return launch_reduce(slot_out, M, int(top_k), N, rw, 1.0f, static_cast<uint16_t*>(out),
+                         stream);
+  return launch_reduce(slot_out, M, int(top_k), N, rw, 1.0f, static_cast<float*>(out), stream);
+}
+
+}  // namespace xk
