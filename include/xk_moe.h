@@ -52,6 +52,12 @@ extern "C" {
 #define XK_DT_FP32 1
 #define XK_DT_NONE (-1) /* "no tensor" for optional weights */
 
+/* int4 flags. Default (0): every dequantised weight is rounded to bf16 before
+ * the contraction, as the reference does. XK_INT4_FAST_DEQUANT contracts the
+ * exact (nibble-8)*scale product instead (cheaper unpack; differs from the
+ * reference by the reference's own bf16 rounding of the weights). */
+#define XK_INT4_FAST_DEQUANT 1
+
 /* Message of the last failed call on this thread ("" if none). */
 const char* xk_last_error(void);
 
@@ -109,8 +115,8 @@ int xk_moe_int4_w4a16(const void* A, int32_t a_dtype, int64_t M, int64_t K,
                       int64_t N, int32_t group_size, const int32_t* topk_ids,
                       const float* topk_w, int64_t top_k,
                       const int32_t* expert_map, int32_t num_global_experts,
-                      int32_t mul_routed_weight, void* out, void* workspace,
-                      int64_t workspace_bytes, hipStream_t stream);
+                      int32_t mul_routed_weight, int32_t flags, void* out,
+                      void* workspace, int64_t workspace_bytes, hipStream_t stream);
 
 /* Stage entry point: only the grouped INT4 GEMM (the reference's
  * _fused_moe_int4_kernel launch, moe_int4_kernel.py:78-272). Consumes the
@@ -126,7 +132,7 @@ int xk_moe_int4_w4a16_gemm(const void* A, int32_t a_dtype, int64_t M, int64_t K,
                            const int32_t* expert_map, int32_t num_global_experts,
                            const int32_t* sorted_token_ids,
                            const int32_t* expert_offsets, float* slot_out,
-                           hipStream_t stream);
+                           int32_t flags, hipStream_t stream);
 
 /* Stage entry point: the weighted top-k combine of per-slot fp32 rows,
  *   out[m, n] = sum_j valid(m,j) * [w[m,j]] * slot_out[m*top_k + j, n]

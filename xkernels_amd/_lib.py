@@ -20,6 +20,7 @@ XK_ERR_LAUNCH = 3
 XK_DT_BF16 = 0
 XK_DT_FP32 = 1
 XK_DT_NONE = -1
+XK_INT4_FAST_DEQUANT = 1
 
 _p = ctypes.c_void_p
 _i32 = ctypes.c_int32
@@ -39,13 +40,13 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "xk_moe_int4_w4a16_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64, _i64]),
     "xk_moe_int4_w4a16": (
         ctypes.c_int,
-        [_p, _i32, _i64, _i64, _p, _p, _i64, _i64, _i32, _p, _p, _i64, _p, _i32, _i32, _p, _p,
-         _i64, _p],
+        [_p, _i32, _i64, _i64, _p, _p, _i64, _i64, _i32, _p, _p, _i64, _p, _i32, _i32, _i32, _p,
+         _p, _i64, _p],
     ),
     "xk_moe_int4_block_size": (_i32, [_i64, _i64, _i64]),
     "xk_moe_int4_w4a16_gemm": (
         ctypes.c_int,
-        [_p, _i32, _i64, _i64, _p, _p, _i64, _i64, _i32, _p, _i64, _p, _i32, _p, _p, _p, _p],
+        [_p, _i32, _i64, _i64, _p, _p, _i64, _i64, _i32, _p, _i64, _p, _i32, _p, _p, _p, _i32, _p],
     ),
     "xk_moe_topk_combine": (
         ctypes.c_int,

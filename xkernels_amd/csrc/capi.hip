@@ -43,7 +43,7 @@ int launch_int4_gemm(const void* A, int a_dtype, int64_t M, int64_t K, const int
                      const uint16_t* scale, int64_t E, int64_t N, int group_size,
                      const int32_t* topk_ids, int64_t top_k, const int32_t* emap,
                      int num_global, const int32_t* sorted_ids, const int32_t* offsets,
-                     float* slot_out, hipStream_t stream);
+                     float* slot_out, int flags, hipStream_t stream);
 int mxfp4_block_size();
 int launch_mxfp4_stage(int stage, const void* A, int a_dtype, const uint8_t* w,
                        const uint8_t* ws, const uint16_t* bias, int64_t E, int64_t K,
@@ -136,11 +136,11 @@ int xk_moe_int4_w4a16_gemm(const void* A, int32_t a_dtype, int64_t M, int64_t K,
                            int32_t group_size, const int32_t* topk_ids, int64_t top_k,
                            const int32_t* expert_map, int32_t num_global_experts,
                            const int32_t* sorted_token_ids, const int32_t* expert_offsets,
-                           float* slot_out, hipStream_t stream) {
+                           float* slot_out, int32_t flags, hipStream_t stream) {
   clear_error();
   return launch_int4_gemm(A, a_dtype, M, K, packed, scale, E, N, group_size, topk_ids, top_k,
                           expert_map, num_global_experts, sorted_token_ids, expert_offsets,
-                          slot_out, stream);
+                          slot_out, flags, stream);
 }
 
 int xk_moe_topk_combine(const float* slot_out, int64_t M, int64_t top_k, int64_t N,
@@ -158,7 +158,7 @@ int xk_moe_int4_w4a16(const void* A, int32_t a_dtype, int64_t M, int64_t K,
                       const int32_t* packed, const uint16_t* scale, int64_t E, int64_t N,
                       int32_t group_size, const int32_t* topk_ids, const float* topk_w,
                       int64_t top_k, const int32_t* expert_map, int32_t num_global_experts,
-                      int32_t mul_routed_weight, void* out, void* workspace,
+                      int32_t mul_routed_weight, int32_t flags, void* out, void* workspace,
                       int64_t workspace_bytes, hipStream_t stream) {
   clear_error();
   if (int rc = check_dtype(a_dtype, "int4 A")) return rc;
@@ -190,7 +190,7 @@ int xk_moe_int4_w4a16(const void* A, int32_t a_dtype, int64_t M, int64_t K,
   }
   if (int rc = launch_int4_gemm(A, a_dtype, M, K, packed, scale, E, N, group_size, topk_ids,
                                 top_k, expert_map, num_global_experts, sorted, offsets,
-                                slot_out, stream))
+                                slot_out, flags, stream))
     return rc;
   return launch_topk_combine(slot_out, M, top_k, N, topk_w, mul_routed_weight, topk_ids,
                              int(E), expert_map, num_global_experts, out, a_dtype, stream);

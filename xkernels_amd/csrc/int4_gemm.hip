@@ -7,7 +7,10 @@
 // with W[e, n, k] = (nibble(e, n, k) - 8) * scale[e, n, k / 32]. The weighted
 // top-k combine runs afterwards (reduce.hip).
 //
-// Stream kernel (bf16 A, group 32) — the decode regime is weight-streaming
+// Two stream kernels (bf16 A, group 32). int4_stream_gemm_rne (default) rounds
+// every dequantised weight to bf16 like the reference; int4_stream_gemm
+// (XK_INT4_FAST_DEQUANT) is described next.
+// Fast stream kernel — the decode regime is weight-streaming
 // bound, so every packed weight byte is read from HBM exactly once:
 //   * one workgroup owns (expert e, 128 output columns) and ALL of e's slots,
 //     taking them 32 at a time, so an expert's weights are streamed once per
@@ -236,6 +239,173 @@ int4_stream_gemm(StreamArgs p) {
   }
 }
 
+// Reference-faithful stream kernel: each weight is dequantised as
+// bf16_rne((n - 8) * s) (v_cvt_f32_ubyte + v_fma_f32 + v_cvt_pk_bf16_f32, the
+// reference's w4a16.py:42-50 rounding) before the MFMA, so the contraction sees
+// the same bf16 weights the reference multiplies. With the scale applied before
+// the MFMA the k order inside an MFMA is free: lane (c, q) loads 16 bytes = one
+// whole 32-k group (group g0 + q of the step) and feeds four MFMAs from it.
+__global__ void __launch_bounds__(256)
+int4_stream_gemm_rne(StreamArgs p) {
+  __shared__ __attribute__((aligned(16))) uint16_t a_lds[kRowsPerPass * kALdsStride];
+  __shared__ int slot_lds[kRowsPerPass];
+  __shared__ int tok_lds[kRowsPerPass];
+
+  const int e = blockIdx.y;
+  const int beg = p.offsets[e], end = p.offsets[e + 1];
+  if (beg >= end) return;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int c16 = lane & 15, q = lane >> 4;
+  const int K = p.K, N = p.N, G = K >> 5, KW = K >> 3;
+  const int n_base = blockIdx.x * kColsPerWG + wave * kColsPerWave;
+
+  const uint32_t* wrow[2];
+  const uint16_t* srow[2];
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    const int n = min(n_base + 16 * c + c16, N - 1);
+    wrow[c] = p.packed + (static_cast<int64_t>(e) * N + n) * KW;
+    srow[c] = p.scale + (static_cast<int64_t>(e) * N + n) * G;
+  }
+  const int st_r = tid >> 3, st_g = tid & 7;
+
+  for (int pass = beg; pass < end; pass += kRowsPerPass) {
+    const int ntiles = min(2, (end - pass) >> 4);
+    __syncthreads();
+    if (tid < kRowsPerPass) {
+      int slot = -1, tok = -1;
+      if (tid < ntiles * 16) {
+        const int s = p.sorted_ids[pass + tid];
+        if (s < p.numel) { slot = s; tok = s / p.top_k; }
+      }
+      slot_lds[tid] = slot;
+      tok_lds[tid] = tok;
+    }
+    __syncthreads();
+    const int my_tok = tok_lds[st_r];
+
+    auto load_a = [&](int g0, uint32_t* areg) {
+      const int g = g0 + st_g;
+      if (my_tok >= 0 && g < G) {
+        const u32x4* src = reinterpret_cast<const u32x4*>(
+            p.A + static_cast<int64_t>(my_tok) * K + g * 32);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const u32x4 v = src[j];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) areg[4 * j + i] = v[i];
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) areg[i] = 0u;
+      }
+    };
+    // weights of groups g0 + 4h + q (h = 0, 1) for both column tiles
+    auto load_w = [&](int g0, u32x4 (*wr)[2], float (*sr)[2]) {
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int g = g0 + 4 * h + q;
+          if (g < G) {
+            wr[c][h] = *reinterpret_cast<const u32x4*>(wrow[c] + g * 4);
+            sr[c][h] = bf16_to_f32(srow[c][g]);
+          } else {
+            wr[c][h] = u32x4{0u, 0u, 0u, 0u};
+            sr[c][h] = 0.f;
+          }
+        }
+    };
+
+    f32x4 acc[2][2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int c = 0; c < 2; ++c) acc[t][c] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    uint32_t areg[16];
+    u32x4 wcur[2][2], wnext[2][2];
+    float scur[2][2], snext[2][2];
+    load_a(0, areg);
+    load_w(0, wcur, scur);
+
+    for (int g0 = 0; g0 < G; g0 += kChunkGroups) {
+      __syncthreads();
+      {
+        u32x4* dst = reinterpret_cast<u32x4*>(a_lds + st_r * kALdsStride + st_g * 32);
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+          dst[s] = u32x4{areg[4 * s], areg[4 * s + 1], areg[4 * s + 2], areg[4 * s + 3]};
+      }
+      __syncthreads();
+      const int gn = g0 + kChunkGroups;
+      if (gn < G) {
+        load_a(gn, areg);
+        load_w(gn, wnext, snext);
+      }
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        if (g0 + 4 * h >= G) break;
+        // dequantise the four words of both column tiles
+        bf16x8 bfrag[2][4];
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+          const float s = scur[c][h], ms = -8.0f * s;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            uint32_t t = wcur[c][h][j] & 0x0F0F0F0Fu;
+            uint32_t u = (wcur[c][h][j] >> 4) & 0x0F0F0F0Fu;
+            // keep the byte-lane form so each nibble converts with v_cvt_f32_ubyteN
+            asm("" : "+v"(t));
+            asm("" : "+v"(u));
+            u32x4 b;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const float lo = fmaf(static_cast<float>((t >> (8 * i)) & 0xFFu), s, ms);
+              const float hi = fmaf(static_cast<float>((u >> (8 * i)) & 0xFFu), s, ms);
+              b[i] = static_cast<uint32_t>(f32_to_bf16(lo)) |
+                     (static_cast<uint32_t>(f32_to_bf16(hi)) << 16);
+            }
+            bfrag[c][j] = __builtin_bit_cast(bf16x8, b);
+          }
+        }
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          if (t >= ntiles) break;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const bf16x8 afrag = *reinterpret_cast<const bf16x8*>(
+                a_lds + (t * 16 + c16) * kALdsStride + (4 * h + q) * 32 + 8 * j);
+#pragma unroll
+            for (int c = 0; c < 2; ++c)
+              acc[t][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(afrag, bfrag[c][j], acc[t][c], 0, 0, 0);
+          }
+        }
+      }
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) { wcur[c][h] = wnext[c][h]; scur[c][h] = snext[c][h]; }
+    }
+
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      if (t >= ntiles) break;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int slot = slot_lds[t * 16 + q * 4 + i];
+        if (slot < 0) continue;
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+          const int n = n_base + 16 * c + c16;
+          if (n < N) p.out[static_cast<int64_t>(slot) * N + n] = acc[t][c][i];
+        }
+      }
+    }
+  }
+}
+
 // One thread per (slot, column); exact dequant rounded to A's dtype.
 template <typename TA>
 __global__ void __launch_bounds__(256)
@@ -282,7 +452,7 @@ int launch_int4_gemm(const void* A, int a_dtype, int64_t M, int64_t K, const int
                      const uint16_t* scale, int64_t E, int64_t N, int group_size,
                      const int32_t* topk_ids, int64_t top_k, const int32_t* emap,
                      int num_global, const int32_t* sorted_ids, const int32_t* offsets,
-                     float* slot_out, hipStream_t stream) {
+                     float* slot_out, int flags, hipStream_t stream) {
   XK_REQUIRE(a_dtype == XK_DT_BF16 || a_dtype == XK_DT_FP32, "int4: bad A dtype %d", a_dtype);
   XK_REQUIRE(M >= 0 && top_k >= 1 && E >= 1 && N >= 1 && K >= 8, "int4: bad sizes");
   XK_REQUIRE(K % 8 == 0, "int4: K=%lld not a multiple of 8", (long long)K);
@@ -299,8 +469,13 @@ int launch_int4_gemm(const void* A, int a_dtype, int64_t M, int64_t K, const int
                  scale, sorted_ids, offsets, slot_out, int(K), int(N), int(numel), int(top_k),
                  int((K / 32) % 8 == 0 && reinterpret_cast<uintptr_t>(scale) % 16 == 0)};
     const dim3 grid(static_cast<unsigned>(cdiv(N, kColsPerWG)), static_cast<unsigned>(E));
-    hipLaunchKernelGGL(int4_stream_gemm, grid, dim3(256), 0, stream, a);
-    XK_CHECK_LAUNCH("int4_stream_gemm");
+    if (flags & XK_INT4_FAST_DEQUANT) {
+      hipLaunchKernelGGL(int4_stream_gemm, grid, dim3(256), 0, stream, a);
+      XK_CHECK_LAUNCH("int4_stream_gemm");
+    } else {
+      hipLaunchKernelGGL(int4_stream_gemm_rne, grid, dim3(256), 0, stream, a);
+      XK_CHECK_LAUNCH("int4_stream_gemm_rne");
+    }
     return XK_OK;
   }
   const int64_t total = numel * N;
