@@ -57,6 +57,9 @@ extern "C" {
  * exact (nibble-8)*scale product instead (cheaper unpack; differs from the
  * reference by the reference's own bf16 rounding of the weights). */
 #define XK_INT4_FAST_DEQUANT 1
+/* Diagnostic: force the non-persistent stream kernels (also used when K is not
+ * a multiple of 512). */
+#define XK_INT4_V1 2
 
 /* Message of the last failed call on this thread ("" if none). */
 const char* xk_last_error(void);
@@ -121,10 +124,14 @@ int xk_moe_int4_w4a16(const void* A, int32_t a_dtype, int64_t M, int64_t K,
 /* Stage entry point: only the grouped INT4 GEMM (the reference's
  * _fused_moe_int4_kernel launch, moe_int4_kernel.py:78-272). Consumes the
  * align outputs built with block_size = xk_moe_int4_block_size(M, top_k, E) and
- * writes un-weighted fp32 per-slot rows slot_out [numel, N] for every routed
- * slot (rows of dropped slots are left untouched). Used by benchmarks to time
- * the GEMM alone. */
+ * writes un-weighted fp32 per-slot rows for every routed slot (rows of dropped
+ * slots are left untouched). The K range may be split: slot_out is
+ * [parts, numel, N] with parts = xk_moe_int4_gemm_parts(...); the partial
+ * planes are summed by xk_moe_topk_combine(..., nparts = parts). Used by
+ * benchmarks to time the GEMM alone. */
 int32_t xk_moe_int4_block_size(int64_t M, int64_t top_k, int64_t E);
+int32_t xk_moe_int4_gemm_parts(int64_t E, int64_t N, int64_t K, int32_t a_dtype,
+                               int32_t group_size, int32_t flags);
 int xk_moe_int4_w4a16_gemm(const void* A, int32_t a_dtype, int64_t M, int64_t K,
                            const int32_t* packed, const uint16_t* scale,
                            int64_t E, int64_t N, int32_t group_size,
@@ -135,14 +142,15 @@ int xk_moe_int4_w4a16_gemm(const void* A, int32_t a_dtype, int64_t M, int64_t K,
                            int32_t flags, hipStream_t stream);
 
 /* Stage entry point: the weighted top-k combine of per-slot fp32 rows,
- *   out[m, n] = sum_j valid(m,j) * [w[m,j]] * slot_out[m*top_k + j, n]
+ *   out[m, n] = sum_j valid(m,j) * [w[m,j]] * sum_p slot_out[p, m*top_k + j, n]
  * where valid drops slots whose expert is not local (expert_map) or out of
  * range; out in out_dtype. */
 int xk_moe_topk_combine(const float* slot_out, int64_t M, int64_t top_k,
                         int64_t N, const float* topk_w, int32_t mul_routed_weight,
                         const int32_t* topk_ids, int32_t num_local_experts,
                         const int32_t* expert_map, int32_t num_global_experts,
-                        void* out, int32_t out_dtype, hipStream_t stream);
+                        void* out, int32_t out_dtype, int32_t nparts,
+                        hipStream_t stream);
 
 /* ---------------------------------------------------------------------------
  * fused_moe_mxfp4 — mxfp4_interface.py:22-100 / mxfp4_reference.py:28-112.

@@ -21,6 +21,7 @@ XK_DT_BF16 = 0
 XK_DT_FP32 = 1
 XK_DT_NONE = -1
 XK_INT4_FAST_DEQUANT = 1
+XK_INT4_V1 = 2
 
 _p = ctypes.c_void_p
 _i32 = ctypes.c_int32
@@ -50,8 +51,9 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     ),
     "xk_moe_topk_combine": (
         ctypes.c_int,
-        [_p, _i64, _i64, _i64, _p, _i32, _p, _i32, _p, _i32, _p, _i32, _p],
+        [_p, _i64, _i64, _i64, _p, _i32, _p, _i32, _p, _i32, _p, _i32, _i32, _p],
     ),
+    "xk_moe_int4_gemm_parts": (_i32, [_i64, _i64, _i64, _i32, _i32, _i32]),
     "xk_moe_mxfp4_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64, _i64]),
     "xk_moe_mxfp4": (
         ctypes.c_int,

@@ -36,7 +36,8 @@ int launch_sum_reduce(const void* y, int y_dtype, int64_t M, int64_t top_k, int6
 int launch_topk_combine(const float* slot_out, int64_t M, int64_t top_k, int64_t N,
                         const float* topk_w, int mul_routed_weight, const int32_t* topk_ids,
                         int num_local, const int32_t* emap, int num_global, void* out,
-                        int out_dtype, hipStream_t stream);
+                        int out_dtype, int nparts, hipStream_t stream);
+int int4_gemm_parts(int64_t E, int64_t N, int64_t K, int a_dtype, int group_size, int flags);
 int int4_block_size();
 bool int4_use_stream(int a_dtype, int group_size, int64_t K);
 int launch_int4_gemm(const void* A, int a_dtype, int64_t M, int64_t K, const int32_t* packed,
@@ -123,12 +124,18 @@ int32_t xk_moe_int4_block_size(int64_t M, int64_t top_k, int64_t E) {
   return int4_block_size();
 }
 
+int32_t xk_moe_int4_gemm_parts(int64_t E, int64_t N, int64_t K, int32_t a_dtype,
+                               int32_t group_size, int32_t flags) {
+  return int4_gemm_parts(E, N, K, a_dtype, group_size, flags);
+}
+
 int64_t xk_moe_int4_w4a16_workspace_bytes(int64_t M, int64_t top_k, int64_t E, int64_t N,
                                           int64_t K) {
-  (void)K;
   const int64_t numel = M * top_k;
   AlignScratch al(numel, int(E), int4_block_size());
-  return al.total + round_up(numel * N * 4);
+  // sized for the largest number of partial planes any mode / dtype uses
+  const int64_t parts = int4_gemm_parts(E, N, K, XK_DT_BF16, 32, 0);
+  return al.total + round_up(parts * numel * N * 4);
 }
 
 int xk_moe_int4_w4a16_gemm(const void* A, int32_t a_dtype, int64_t M, int64_t K,
@@ -147,11 +154,11 @@ int xk_moe_topk_combine(const float* slot_out, int64_t M, int64_t top_k, int64_t
                         const float* topk_w, int32_t mul_routed_weight,
                         const int32_t* topk_ids, int32_t num_local_experts,
                         const int32_t* expert_map, int32_t num_global_experts, void* out,
-                        int32_t out_dtype, hipStream_t stream) {
+                        int32_t out_dtype, int32_t nparts, hipStream_t stream) {
   clear_error();
   return launch_topk_combine(slot_out, M, top_k, N, topk_w, mul_routed_weight, topk_ids,
                              num_local_experts, expert_map, num_global_experts, out, out_dtype,
-                             stream);
+                             nparts, stream);
 }
 
 int xk_moe_int4_w4a16(const void* A, int32_t a_dtype, int64_t M, int64_t K,
@@ -193,7 +200,8 @@ int xk_moe_int4_w4a16(const void* A, int32_t a_dtype, int64_t M, int64_t K,
                                 slot_out, flags, stream))
     return rc;
   return launch_topk_combine(slot_out, M, top_k, N, topk_w, mul_routed_weight, topk_ids,
-                             int(E), expert_map, num_global_experts, out, a_dtype, stream);
+                             int(E), expert_map, num_global_experts, out, a_dtype,
+                             int4_gemm_parts(E, N, K, a_dtype, group_size, flags), stream);
 }
 
 int64_t xk_moe_mxfp4_workspace_bytes(int64_t M, int64_t top_k, int64_t E, int64_t hidden,
@@ -243,7 +251,7 @@ int xk_moe_mxfp4(const void* A, int32_t a_dtype, int64_t M, int64_t hidden, cons
                           offsets, numel, top_k, 0.f, nullptr, slot_out, stream);
   if (rc) return rc;
   return launch_topk_combine(slot_out, M, top_k, hidden, topk_w, mul_routed_weight, topk_ids,
-                             int(E), expert_map, num_global_experts, out, a_dtype, stream);
+                             int(E), expert_map, num_global_experts, out, a_dtype, 1, stream);
 }
 
 }  // extern "C"

@@ -32,6 +32,8 @@
 // Simple kernel: any dtype / group size, one thread per (slot, column), exact
 // dequant rounded to A's dtype like the reference. Correctness fallback for the
 // fp32 sweep points and unusual group sizes.
+#include <algorithm>
+
 #include "common.h"
 
 namespace xk {
@@ -406,6 +408,356 @@ int4_stream_gemm_rne(StreamArgs p) {
   }
 }
 
+// ------------------------------------------------------------------------------
+// Persistent stream kernel (K % 256 == 0), the production decode path. Same
+// math as the two kernels above, restructured for bytes in flight:
+//   * work items are (active expert, 128-column block); the grid is sized to
+//     the machine (2 workgroups per CU) and each workgroup walks items
+//     blockIdx.x, blockIdx.x + gridDim.x, ...; the active-expert list is
+//     rebuilt per item from the padded offsets with one ballot per 64 experts
+//     (no host sync);
+//   * every lane loads 16 bytes (one whole 32-k group) per column tile and
+//     chunk half, from a 4-deep register ring (weights requested 3 chunks
+//     ahead); activations go through two LDS buffers (one barrier per chunk);
+//     every global load is unconditional (clamped indices) so the compiler can
+//     count outstanding loads instead of draining them;
+//   * group scales arrive in full 128-byte lines: each wave keeps a
+//     double-buffered LDS copy of its 32 rows' scales for 8 chunks, refilled
+//     8 bytes per lane per chunk (fetching a scale line piecewise per chunk
+//     lets the weight stream evict it between visits);
+//   * activations are staged with the k-permutation the nibble unpack
+//     produces and a 544-byte row pitch, so the MFMA operand reads are
+//     bank-conflict free;
+//   * RNE mode dequantises every weight to bf16_rne((n-8)*s) before the MFMA
+//     (reference rounding). FAST mode transposes the four words of a group
+//     across the four lane groups with v_permlane32_swap / v_permlane16_swap
+//     so one MFMA contracts one group, unpacks nibbles to bf16 (128+n) with
+//     v_and_or_b32, subtracts 136*sum(a) with a second MFMA against a constant
+//     -136 operand (shared by both column tiles) and applies the group scale
+//     to the MFMA result.
+enum class Int4Mode { kRne, kFast };
+
+constexpr int kV2Rows = 32;  // two 16-row MFMA tiles per pass
+constexpr int kV2Stride = kChunkK + 16;  // bf16 per LDS row: 544 B, bank-staggered rows
+
+struct V2Args {
+  StreamArgs s;
+  int num_experts;
+};
+
+__device__ __forceinline__ int find_active_expert(const int32_t* offsets, int E, int rank) {
+  // index of the rank-th expert with a non-empty padded range (all lanes agree)
+  const int lane = threadIdx.x & 63;
+  int seen = 0;
+  for (int base = 0; base < E; base += 64) {
+    const int e = base + lane;
+    const bool act = e < E && offsets[e + 1] > offsets[e];
+    const uint64_t m = __ballot(act);
+    const int cnt = __popcll(m);
+    if (rank < seen + cnt) {
+      uint64_t mm = m;
+      for (int r = rank - seen; r > 0; --r) mm &= mm - 1;  // drop lower set bits
+      return base + __ffsll(static_cast<long long>(mm)) - 1;
+    }
+    seen += cnt;
+  }
+  return -1;
+}
+
+__device__ __forceinline__ int count_active_experts(const int32_t* offsets, int E) {
+  const int lane = threadIdx.x & 63;
+  int n = 0;
+  for (int base = 0; base < E; base += 64) {
+    const int e = base + lane;
+    n += __popcll(__ballot(e < E && offsets[e + 1] > offsets[e]));
+  }
+  return n;
+}
+
+// 4x4 transpose of 32-bit words across the four 16-lane groups:
+// out[j] in lane group q = in[q] of lane group j.
+__device__ __forceinline__ void transpose4(u32x4& w) {
+  auto a = __builtin_amdgcn_permlane32_swap(w[0], w[2], false, false);
+  auto b = __builtin_amdgcn_permlane32_swap(w[1], w[3], false, false);
+  auto c = __builtin_amdgcn_permlane16_swap(a[0], b[0], false, false);
+  auto d = __builtin_amdgcn_permlane16_swap(a[1], b[1], false, false);
+  w = u32x4{c[0], c[1], d[0], d[1]};
+}
+
+// (x & m) | k in one v_and_or_b32 (the compiler otherwise splits it in two).
+__device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t m, uint32_t k) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "v"(m), "v"(k));
+  return r;
+}
+
+// 8 nibbles of `w` (low nibble = lowest k) -> 8 bf16 = bf16_rne((n - 8) * s),
+// the reference's dequant rounding. Each nibble pair becomes two fp16 values
+// 1024 + n (one v_and_or_b32); v_fma_mix_f32 forms (1024 + n) * s - 1032 * s
+// exactly in fp32 (both terms fit 24 bits), and v_cvt_pk_bf16_f32 rounds.
+// Output element order: n0 n4 n1 n5 n2 n6 n3 n7 (pairs d, d + 4).
+__device__ __forceinline__ bf16x8 dequant_rne(uint32_t w, float s, float ms1032, uint32_t mask) {
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  typedef float f2 __attribute__((ext_vector_type(2)));
+  typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+  u32x4 b;
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    const h2 x = __builtin_bit_cast(h2, and_or(w >> (4 * d), mask, 0x64006400u));
+    const f2 v = {fmaf(static_cast<float>(x[0]), s, ms1032), fmaf(static_cast<float>(x[1]), s, ms1032)};
+    b[d] = __builtin_bit_cast(uint32_t, __builtin_convertvector(v, b2));
+  }
+  return __builtin_bit_cast(bf16x8, b);
+}
+
+// 8 nibbles -> bf16 (128 + n), same element order as dequant_rne.
+__device__ __forceinline__ bf16x8 dequant_magic(uint32_t w, uint32_t mask) {
+  u32x4 b;
+#pragma unroll
+  for (int d = 0; d < 4; ++d) b[d] = and_or(w >> (4 * d), mask, 0x43004300u);
+  return __builtin_bit_cast(bf16x8, b);
+}
+
+template <Int4Mode MODE>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+int4_stream_v2(V2Args args) {
+  constexpr bool kFast = MODE == Int4Mode::kFast;
+  constexpr int kWRing = 4;       // weight chunks in registers (prefetch distance 3)
+  constexpr int kSuper = 8;       // chunks per scale superchunk: 64 groups = 128 B per row
+  constexpr int kSStride = 72;    // bf16 per scale row in LDS (128 B + 16 B pad)
+  __shared__ __attribute__((aligned(16))) uint16_t a_lds[2][kV2Rows * kV2Stride];
+  __shared__ __attribute__((aligned(16))) uint16_t s_lds[kWaves][2][32 * kSStride];
+  __shared__ int slot_lds[kV2Rows];
+  __shared__ int tok_lds[kV2Rows];
+  const StreamArgs& p = args.s;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int c16 = lane & 15, q = lane >> 4;
+  const int K = p.K, N = p.N, G = K >> 5, KW = K >> 3;
+  const int nb = (N + kColsPerWG - 1) / kColsPerWG;
+  const int nchunks = G / kChunkGroups;
+  const int items = count_active_experts(p.offsets, args.num_experts) * nb;
+  const int st_r = tid >> 3, st_g = tid & 7;
+  const uint32_t kNibMask = 0x000F000Fu;
+  const bf16x8 neg136 = __builtin_bit_cast(bf16x8, u32x4{0xC308C308u, 0xC308C308u, 0xC308C308u, 0xC308C308u});
+
+  for (int item = blockIdx.x; item < items; item += gridDim.x) {
+    const int e = find_active_expert(p.offsets, args.num_experts, item / nb);
+    const int n_base = (item % nb) * kColsPerWG + wave * kColsPerWave;
+    const int beg = p.offsets[e], end = p.offsets[e + 1];
+    const uint32_t* wrow[2];
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      const int n = min(n_base + 16 * c + c16, N - 1);
+      wrow[c] = p.packed + (static_cast<int64_t>(e) * N + n) * KW + q * 4;
+    }
+    // scale pieces: lane -> (row lane/2 of the wave's 32 rows, 8-byte half lane&1)
+    const int sp_row = lane >> 1, sp_half = lane & 1;
+    const uint16_t* sp_src =
+        p.scale + (static_cast<int64_t>(e) * N + min(n_base + sp_row, N - 1)) * G + sp_half * 4;
+
+    for (int pass = beg; pass < end; pass += kV2Rows) {
+      const int ntiles = min(2, (end - pass) >> 4);
+      __syncthreads();  // previous pass / item done with LDS
+      if (tid < kV2Rows) {
+        int slot = -1, tok = -1;
+        if (tid < ntiles * 16) {
+          const int sidx = p.sorted_ids[pass + tid];
+          if (sidx < p.numel) { slot = sidx; tok = sidx / p.top_k; }
+        }
+        slot_lds[tid] = slot;
+        tok_lds[tid] = tok;
+      }
+      __syncthreads();
+      // Rows without a token read row 0: MFMA rows are independent and those
+      // rows are never stored, so no branch (and no load-counter drain).
+      const int my_tok = max(tok_lds[st_r], 0);
+      const u32x4* a_src =
+          reinterpret_cast<const u32x4*>(p.A + static_cast<int64_t>(my_tok) * K) + st_g * 4;
+
+      // Every global load below is unconditional (indices clamped) so the
+      // compiler keeps counting outstanding loads across the ring.
+      auto load_a = [&](int chunk, u32x4* ar) {
+        chunk = min(chunk, nchunks - 1);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) ar[j] = a_src[chunk * (kChunkK / 8) + j];
+      };
+      auto store_a = [&](int buf, const u32x4* ar) {
+        // Both dequant forms emit the pair order (d, d + 4); stage A to match.
+        // 16-byte piece (group g = st_g, subgroup j) of a row goes to dword
+        //   RNE : (g >> 2) * 64 + j * 16 + (g & 3) * 4   (lane q reads group 4h+q)
+        //   FAST: (g >> 2) * 64 + (g & 3) * 16 + j * 4   (lane q reads subgroup q)
+        // so the 16-byte reads of one MFMA are 4 dwords apart across lane groups
+        // and the 16 rows are 136 dwords apart: bank-conflict free.
+        uint32_t* row = reinterpret_cast<uint32_t*>(&a_lds[buf][st_r * kV2Stride]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          uint32_t in[4] = {ar[j][0], ar[j][1], ar[j][2], ar[j][3]}, o[4];
+          perm8(in, o);
+          const int off = (st_g >> 2) * 64 + (kFast ? (st_g & 3) * 16 + j * 4 : j * 16 + (st_g & 3) * 4);
+          *reinterpret_cast<u32x4*>(row + off) = u32x4{o[0], o[1], o[2], o[3]};
+        }
+      };
+      auto load_w = [&](int chunk, u32x4 (&wr)[2][2]) {
+        chunk = min(chunk, nchunks - 1);
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+          for (int h = 0; h < 2; ++h)
+            wr[c][h] = *reinterpret_cast<const u32x4*>(wrow[c] + (chunk * kChunkGroups + 4 * h) * 4);
+      };
+      // 8 bytes of scale superchunk `sc`, piece `pc` (16-byte slice of the row)
+      auto load_spiece = [&](int sc, int pc) -> uint2 {
+        const int off = min(sc * 64 + pc * 8, G - 4);
+        return *reinterpret_cast<const uint2*>(sp_src + off);
+      };
+      // (index the __shared__ array directly: a pointer variable would turn
+      // these into flat accesses, which also count as vector-memory loads)
+      auto store_spiece = [&](int sc, int pc, uint2 v) {
+        *reinterpret_cast<uint2*>(&s_lds[wave][sc & 1][sp_row * kSStride + pc * 8 + sp_half * 4]) = v;
+      };
+
+      f32x4 acc[2][2];
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int c = 0; c < 2; ++c) acc[t][c] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+      auto compute = [&](int buf, int chunk, const u32x4 (&wr)[2][2]) {
+        // the chunk's 8 group scales of both column rows
+        uint32_t sr[2][4];
+        const int sbuf = (chunk / kSuper) & 1;
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+          const u32x4 v = *reinterpret_cast<const u32x4*>(
+              &s_lds[wave][sbuf][(16 * c + c16) * kSStride + (chunk % kSuper) * 8]);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) sr[c][i] = v[i];
+        }
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          if constexpr (kFast) {
+            u32x4 w[2];
+#pragma unroll
+            for (int c = 0; c < 2; ++c) { w[c] = wr[c][h]; transpose4(w[c]); }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              bf16x8 bfrag[2];
+              float sc[2];
+#pragma unroll
+              for (int c = 0; c < 2; ++c) {
+                bfrag[c] = dequant_magic(w[c][j], kNibMask);
+                const uint32_t sw = sr[c][(4 * h + j) >> 1];
+                sc[c] = __uint_as_float(((4 * h + j) & 1) ? (sw & 0xFFFF0000u) : (sw << 16));
+              }
+#pragma unroll
+              for (int t = 0; t < 2; ++t) {
+                if (t >= ntiles) break;
+                const bf16x8 afrag = *reinterpret_cast<const bf16x8*>(
+                    &a_lds[buf][(t * 16 + c16) * kV2Stride + 2 * (h * 64 + j * 16 + q * 4)]);
+                const f32x4 d2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                    afrag, neg136, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+#pragma unroll
+                for (int c = 0; c < 2; ++c) {
+                  const f32x4 d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(afrag, bfrag[c], d2, 0, 0, 0);
+#pragma unroll
+                  for (int i = 0; i < 4; ++i) acc[t][c][i] = fmaf(sc[c], d[i], acc[t][c][i]);
+                }
+              }
+            }
+          } else {
+            float s[2], ms[2];
+#pragma unroll
+            for (int c = 0; c < 2; ++c) {
+              // scale of group 4h + q: word 2h + (q >> 1), half q & 1
+              const uint32_t lo = (q & 2) ? sr[c][2 * h + 1] : sr[c][2 * h];
+              s[c] = __uint_as_float((q & 1) ? (lo & 0xFFFF0000u) : (lo << 16));
+              ms[c] = -1032.0f * s[c];
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              bf16x8 bfrag[2];
+#pragma unroll
+              for (int c = 0; c < 2; ++c) bfrag[c] = dequant_rne(wr[c][h][j], s[c], ms[c], kNibMask);
+#pragma unroll
+              for (int t = 0; t < 2; ++t) {
+                if (t >= ntiles) break;
+                const bf16x8 afrag = *reinterpret_cast<const bf16x8*>(
+                    &a_lds[buf][(t * 16 + c16) * kV2Stride + 2 * (h * 64 + j * 16 + q * 4)]);
+#pragma unroll
+                for (int c = 0; c < 2; ++c)
+                  acc[t][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(afrag, bfrag[c], acc[t][c], 0, 0, 0);
+              }
+            }
+          }
+        }
+      };
+
+      // Prologue: scale superchunk 0 and activation chunk 0 in LDS, A(1) and
+      // W(0..2) in flight.
+      u32x4 areg[4];
+      u32x4 w0[2][2], w1[2][2], w2[2][2], w3[2][2];
+#pragma unroll
+      for (int pc = 0; pc < kSuper; ++pc) store_spiece(0, pc, load_spiece(0, pc));
+      load_a(0, areg);
+      store_a(0, areg);
+      load_a(1, areg);
+      load_w(0, w0);
+      load_w(1, w1);
+      load_w(2, w2);
+      uint2 spiece = make_uint2(0u, 0u);
+      // step c: A(c+1) -> LDS buffer (c+1)&1 (freed by compute(c-1)); the scale
+      // piece loaded at step c-1 -> LDS; request A(c+2), scale piece (c/8+1, c%8)
+      // and W(c+3); compute chunk c.
+      auto step = [&](int c, const u32x4 (&wc)[2][2], u32x4 (&wn)[2][2]) {
+        __syncthreads();
+        store_a((c + 1) & 1, areg);
+        // LDS operations of one wave execute in order, so the other lanes'
+        // reads in compute() see this piece without a barrier.
+        if (c > 0) store_spiece((c - 1) / kSuper + 1, (c - 1) % kSuper, spiece);
+        load_a(c + 2, areg);
+        spiece = load_spiece(c / kSuper + 1, c % kSuper);
+        load_w(c + 3, wn);
+        if (c < nchunks) compute(c & 1, c, wc);
+      };
+      for (int c = 0; c < nchunks; c += kWRing) {
+        step(c, w0, w3);
+        step(c + 1, w1, w0);
+        step(c + 2, w2, w1);
+        step(c + 3, w3, w2);
+      }
+
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        if (t >= ntiles) break;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int slot = slot_lds[t * 16 + q * 4 + i];
+          if (slot < 0) continue;
+#pragma unroll
+          for (int c = 0; c < 2; ++c) {
+            const int n = n_base + 16 * c + c16;
+            if (n < N) p.out[static_cast<int64_t>(slot) * N + n] = acc[t][c][i];
+          }
+        }
+      }
+    }
+  }
+}
+
+int device_cu_count() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
 // One thread per (slot, column); exact dequant rounded to A's dtype.
 template <typename TA>
 __global__ void __launch_bounds__(256)
@@ -448,6 +800,13 @@ bool int4_use_stream(int a_dtype, int group_size, int64_t K) {
   return a_dtype == XK_DT_BF16 && group_size == 32 && K % 32 == 0 && K >= 32;
 }
 
+// Number of fp32 partial planes the grouped GEMM writes (every kernel here
+// contracts the full K range per output, so one).
+int int4_gemm_parts(int64_t E, int64_t N, int64_t K, int a_dtype, int group_size, int flags) {
+  (void)E; (void)N; (void)K; (void)a_dtype; (void)group_size; (void)flags;
+  return 1;
+}
+
 int launch_int4_gemm(const void* A, int a_dtype, int64_t M, int64_t K, const int32_t* packed,
                      const uint16_t* scale, int64_t E, int64_t N, int group_size,
                      const int32_t* topk_ids, int64_t top_k, const int32_t* emap,
@@ -468,6 +827,17 @@ int launch_int4_gemm(const void* A, int a_dtype, int64_t M, int64_t K, const int
     StreamArgs a{static_cast<const uint16_t*>(A), reinterpret_cast<const uint32_t*>(packed),
                  scale, sorted_ids, offsets, slot_out, int(K), int(N), int(numel), int(top_k),
                  int((K / 32) % 8 == 0 && reinterpret_cast<uintptr_t>(scale) % 16 == 0)};
+    if (K % 256 == 0 && a.scale_vec && !(flags & XK_INT4_V1)) {
+      V2Args v2{a, int(E)};
+      const int64_t items = E * cdiv(N, kColsPerWG);
+      const dim3 g2(static_cast<unsigned>(std::min<int64_t>(items, 2 * device_cu_count())));
+      if (flags & XK_INT4_FAST_DEQUANT)
+        hipLaunchKernelGGL((int4_stream_v2<Int4Mode::kFast>), g2, dim3(256), 0, stream, v2);
+      else
+        hipLaunchKernelGGL((int4_stream_v2<Int4Mode::kRne>), g2, dim3(256), 0, stream, v2);
+      XK_CHECK_LAUNCH("int4_stream_v2");
+      return XK_OK;
+    }
     const dim3 grid(static_cast<unsigned>(cdiv(N, kColsPerWG)), static_cast<unsigned>(E));
     if (flags & XK_INT4_FAST_DEQUANT) {
       hipLaunchKernelGGL(int4_stream_gemm, grid, dim3(256), 0, stream, a);

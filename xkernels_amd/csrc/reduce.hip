@@ -76,10 +76,12 @@ struct RowWeights {
   }
 };
 
+// y may hold `nparts` planes (partial sums over K) `pstride` elements apart;
+// they are added before weighting.
 template <typename Tin, typename Tout, int VEC, int KFIX>
 __global__ void __launch_bounds__(256)
 topk_reduce(const Tin* __restrict__ y, int64_t M, int top_k_rt, int64_t H, RowWeights rw,
-            float scale, Tout* __restrict__ out) {
+            float scale, Tout* __restrict__ out, int nparts, int64_t pstride) {
   const int top_k = KFIX > 0 ? KFIX : top_k_rt;
   const int64_t chunks_per_row = H / VEC;
   const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -100,6 +102,15 @@ topk_reduce(const Tin* __restrict__ y, int64_t M, int top_k_rt, int64_t H, RowWe
       ok[k] = rw.valid(m * top_k + k);
       vec_io<Tin, VEC>::load(src + k * H, v[k]);
     }
+    for (int p = 1; p < nparts; ++p) {
+#pragma unroll
+      for (int k = 0; k < KFIX; ++k) {
+        float t[VEC];
+        vec_io<Tin, VEC>::load(src + p * pstride + k * H, t);
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) v[k][i] += t[i];
+      }
+    }
 #pragma unroll
     for (int k = 0; k < KFIX; ++k)
 #pragma unroll
@@ -110,6 +121,12 @@ topk_reduce(const Tin* __restrict__ y, int64_t M, int top_k_rt, int64_t H, RowWe
       float v[VEC];
       const float wk = rw.get(m * top_k + k);
       vec_io<Tin, VEC>::load(src + k * H, v);
+      for (int p = 1; p < nparts; ++p) {
+        float t[VEC];
+        vec_io<Tin, VEC>::load(src + p * pstride + k * H, t);
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) v[i] += t[i];
+      }
 #pragma unroll
       for (int i = 0; i < VEC; ++i) acc[i] += v[i] * wk;
     }
@@ -121,7 +138,7 @@ topk_reduce(const Tin* __restrict__ y, int64_t M, int top_k_rt, int64_t H, RowWe
 
 template <typename Tin, typename Tout, int VEC>
 int launch_vec(const Tin* y, int64_t M, int top_k, int64_t H, const RowWeights& rw,
-               float scale, Tout* out, hipStream_t stream) {
+               float scale, Tout* out, int nparts, int64_t pstride, hipStream_t stream) {
   const int64_t n = M * (H / VEC);
   if (n == 0) return XK_OK;
   const dim3 grid(static_cast<unsigned>(cdiv(n, 256))), block(256);
@@ -129,13 +146,13 @@ int launch_vec(const Tin* y, int64_t M, int top_k, int64_t H, const RowWeights& 
 #define XK_K(K)                                                                      \
   case K:                                                                            \
     hipLaunchKernelGGL((topk_reduce<Tin, Tout, VEC, K>), grid, block, 0, stream, y, M, \
-                       top_k, H, rw, scale, out);                                    \
+                       top_k, H, rw, scale, out, nparts, pstride);                   \
     break;
     XK_K(1) XK_K(2) XK_K(4) XK_K(6) XK_K(8)
 #undef XK_K
     default:
       hipLaunchKernelGGL((topk_reduce<Tin, Tout, VEC, 0>), grid, block, 0, stream, y, M,
-                         top_k, H, rw, scale, out);
+                         top_k, H, rw, scale, out, nparts, pstride);
   }
   XK_CHECK_LAUNCH("topk_reduce");
   return XK_OK;
@@ -143,11 +160,13 @@ int launch_vec(const Tin* y, int64_t M, int top_k, int64_t H, const RowWeights& 
 
 template <typename Tin, typename Tout>
 int launch_reduce(const Tin* y, int64_t M, int top_k, int64_t H, const RowWeights& rw,
-                  float scale, Tout* out, hipStream_t stream) {
+                  float scale, Tout* out, hipStream_t stream, int nparts = 1,
+                  int64_t pstride = 0) {
   const bool aligned = (reinterpret_cast<uintptr_t>(y) % 16 == 0) &&
-                       (reinterpret_cast<uintptr_t>(out) % 16 == 0);
-  if (H % 8 == 0 && aligned) return launch_vec<Tin, Tout, 8>(y, M, top_k, H, rw, scale, out, stream);
-  return launch_vec<Tin, Tout, 1>(y, M, top_k, H, rw, scale, out, stream);
+                       (reinterpret_cast<uintptr_t>(out) % 16 == 0) && (pstride % 8 == 0);
+  if (H % 8 == 0 && aligned)
+    return launch_vec<Tin, Tout, 8>(y, M, top_k, H, rw, scale, out, nparts, pstride, stream);
+  return launch_vec<Tin, Tout, 1>(y, M, top_k, H, rw, scale, out, nparts, pstride, stream);
 }
 
 }  // namespace
@@ -172,7 +191,8 @@ int launch_sum_reduce(const void* y, int y_dtype, int64_t M, int64_t top_k, int6
 int launch_topk_combine(const float* slot_out, int64_t M, int64_t top_k, int64_t N,
                         const float* topk_w, int mul_routed_weight, const int32_t* topk_ids,
                         int num_local, const int32_t* emap, int num_global, void* out,
-                        int out_dtype, hipStream_t stream) {
+                        int out_dtype, int nparts, hipStream_t stream) {
+  XK_REQUIRE(nparts >= 1 && nparts <= 64, "combine: nparts=%d outside [1, 64]", nparts);
   XK_REQUIRE(out_dtype == XK_DT_BF16 || out_dtype == XK_DT_FP32, "combine: bad out dtype %d",
              out_dtype);
   XK_REQUIRE(!mul_routed_weight || topk_w, "combine: null topk_w");
@@ -180,10 +200,12 @@ int launch_topk_combine(const float* slot_out, int64_t M, int64_t top_k, int64_t
              (long long)top_k);
   const RowWeights rw{mul_routed_weight ? topk_w : nullptr, XK_DT_FP32, topk_ids, emap,
                       num_global, num_local};
+  const int64_t pstride = M * top_k * N;
   if (out_dtype == XK_DT_BF16)
     return launch_reduce(slot_out, M, int(top_k), N, rw, 1.0f, static_cast<uint16_t*>(out),
-                         stream);
-  return launch_reduce(slot_out, M, int(top_k), N, rw, 1.0f, static_cast<float*>(out), stream);
+                         stream, nparts, pstride);
+  return launch_reduce(slot_out, M, int(top_k), N, rw, 1.0f, static_cast<float*>(out), stream,
+                       nparts, pstride);
 }
 
 }  // namespace xk
