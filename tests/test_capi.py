@@ -1,0 +1,171 @@
+"""The C ABI of libxk_moe.so without a GPU: the library loads, it exports every
+function include/xk_moe.h declares (and the ctypes table binds exactly those),
+the pure-host size queries return the documented sizes, and argument checks
+reject bad calls with XK_ERR_INVALID / XK_ERR_WORKSPACE before any HIP call."""
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from xkernels_amd import _lib
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "xk_moe.h"
+
+
+def _declared() -> set[str]:
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return set(re.findall(r"\b(xk_\w+)\s*\(", text))
+
+
+def _defines() -> dict[str, int]:
+    return {k: int(v) for k, v in re.findall(r"#define\s+(XK_\w+)\s+\(?(-?\d+)\)?", HEADER.read_text())}
+
+
+def test_header_matches_binding_table():
+    assert _declared() == set(_lib.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(str(_lib.LIB_PATH))
+    missing = [n for n in sorted(_declared()) if not hasattr(lib, n)]
+    assert not missing
+
+
+def test_constants_match_header():
+    d = _defines()
+    for name in ("XK_OK", "XK_ERR_INVALID", "XK_ERR_WORKSPACE", "XK_ERR_LAUNCH", "XK_DT_BF16",
+                 "XK_DT_FP32", "XK_DT_NONE", "XK_INT4_FAST_DEQUANT", "XK_INT4_V1"):
+        assert getattr(_lib, name) == d[name], name
+
+
+def test_version_and_empty_error():
+    lib = _lib.load()
+    assert lib.xk_abi_version() == 100
+    assert isinstance(_lib.last_error(), str)
+
+
+def _pad(numel, E, bs):
+    return numel + (E + 1) * (bs - 1)
+
+
+def test_size_queries():
+    bs = _lib.query("xk_moe_int4_block_size", 64, 8, 48)
+    assert bs >= 1
+    assert _lib.query("xk_moe_int4_gemm_parts", 48, 4096, 7168, _lib.XK_DT_BF16, 32, 0) >= 1
+    assert _lib.query("xk_moe_align_workspace_bytes", 512, 48) >= 0
+    ws = _lib.query("xk_moe_int4_w4a16_workspace_bytes", 64, 8, 48, 4096, 7168)
+    # at least the align outputs plus one fp32 row per routed slot
+    assert ws >= 4 * (_pad(512, 48, bs) + 49) + 512 * 4096 * 4
+    assert ws % 256 == 0
+    wm = _lib.query("xk_moe_mxfp4_workspace_bytes", 48, 6, 256, 4096, 512)
+    assert wm >= 288 * 512 * 2 + 288 * 4096 * 4
+
+
+def _rc(name, *args):
+    return getattr(_lib.load(), name)(*args)
+
+
+FAKE = ctypes.c_void_p(0x1000)  # never dereferenced: every case fails validation first
+
+
+def test_align_rejects_bad_arguments():
+    base = dict(ids=FAKE, numel=8, E=4, bs=4, emap=None, ng=0, s=FAKE, e=FAKE, n=FAKE, off=None,
+                ws=FAKE, wsb=1 << 20, stream=None)
+
+    def call(**kw):
+        a = {**base, **kw}
+        return _rc("xk_moe_align_block_size", a["ids"], a["numel"], a["E"], a["bs"], a["emap"], a["ng"],
+                   a["s"], a["e"], a["n"], a["off"], a["ws"], a["wsb"], a["stream"])
+
+    assert call(E=0) == _lib.XK_ERR_INVALID
+    assert call(E=100000) == _lib.XK_ERR_INVALID
+    assert "align" in _lib.last_error()
+    assert call(bs=0) == _lib.XK_ERR_INVALID
+    assert call(numel=-1) == _lib.XK_ERR_INVALID
+    assert call(s=None) == _lib.XK_ERR_INVALID
+    assert call(ids=None) == _lib.XK_ERR_INVALID
+    assert call(emap=FAKE, ng=0) == _lib.XK_ERR_INVALID
+
+
+def test_sum_reduce_rejects_bad_arguments():
+    assert _rc("xk_moe_sum_reduce", FAKE, 7, 4, 2, 8, None, 0, 1.0, FAKE, None) == _lib.XK_ERR_INVALID
+    assert _rc("xk_moe_sum_reduce", FAKE, 0, 4, 2, 8, FAKE, 9, 1.0, FAKE, None) == _lib.XK_ERR_INVALID
+    assert _rc("xk_moe_sum_reduce", None, 0, 4, 2, 8, None, 0, 1.0, FAKE, None) == _lib.XK_ERR_INVALID
+    assert _rc("xk_moe_sum_reduce", FAKE, 0, -1, 2, 8, None, 0, 1.0, FAKE, None) == _lib.XK_ERR_INVALID
+    assert _rc("xk_moe_sum_reduce", FAKE, 0, 4, 2000, 8, None, 0, 1.0, FAKE, None) == _lib.XK_ERR_INVALID
+
+
+def _int4(**kw):
+    a = dict(A=FAKE, dt=0, M=4, K=64, packed=FAKE, scale=FAKE, E=2, N=16, gs=32, ids=FAKE, w=FAKE,
+             k=2, emap=None, ng=0, mul=1, flags=0, out=FAKE, ws=FAKE, wsb=1 << 30, stream=None)
+    a.update(kw)
+    return _rc("xk_moe_int4_w4a16", a["A"], a["dt"], a["M"], a["K"], a["packed"], a["scale"], a["E"],
+               a["N"], a["gs"], a["ids"], a["w"], a["k"], a["emap"], a["ng"], a["mul"], a["flags"],
+               a["out"], a["ws"], a["wsb"], a["stream"])
+
+
+def test_int4_rejects_bad_arguments():
+    assert _int4(dt=5) == _lib.XK_ERR_INVALID
+    assert _int4(k=0) == _lib.XK_ERR_INVALID
+    assert _int4(out=None) == _lib.XK_ERR_INVALID
+    assert _int4(packed=None) == _lib.XK_ERR_INVALID
+    assert _int4(w=None) == _lib.XK_ERR_INVALID
+    assert _int4(wsb=16) == _lib.XK_ERR_WORKSPACE
+    assert "workspace" in _lib.last_error()
+    assert _int4(ws=None) == _lib.XK_ERR_WORKSPACE
+    assert _int4(M=0, A=None, out=None) == _lib.XK_OK  # empty batch: nothing to launch
+
+
+def test_int4_gemm_stage_rejects_bad_arguments():
+    def g(**kw):
+        a = dict(A=FAKE, dt=0, M=4, K=64, packed=FAKE, scale=FAKE, E=2, N=16, gs=32, ids=FAKE, k=2,
+                 emap=None, ng=0, s=FAKE, off=FAKE, out=FAKE, flags=0, stream=None)
+        a.update(kw)
+        return _rc("xk_moe_int4_w4a16_gemm", a["A"], a["dt"], a["M"], a["K"], a["packed"], a["scale"],
+                   a["E"], a["N"], a["gs"], a["ids"], a["k"], a["emap"], a["ng"], a["s"], a["off"],
+                   a["out"], a["flags"], a["stream"])
+    assert g(K=60) == _lib.XK_ERR_INVALID
+    assert g(gs=48) == _lib.XK_ERR_INVALID
+    assert g(dt=3) == _lib.XK_ERR_INVALID
+
+
+def test_combine_rejects_bad_arguments():
+    def c(**kw):
+        a = dict(y=FAKE, M=4, k=2, N=16, w=FAKE, mul=1, ids=FAKE, nl=2, emap=None, ng=0, out=FAKE,
+                 odt=0, parts=1, stream=None)
+        a.update(kw)
+        return _rc("xk_moe_topk_combine", a["y"], a["M"], a["k"], a["N"], a["w"], a["mul"], a["ids"],
+                   a["nl"], a["emap"], a["ng"], a["out"], a["odt"], a["parts"], a["stream"])
+    assert c(parts=0) == _lib.XK_ERR_INVALID
+    assert c(parts=65) == _lib.XK_ERR_INVALID
+    assert c(odt=4) == _lib.XK_ERR_INVALID
+    assert c(w=None) == _lib.XK_ERR_INVALID
+    assert c(k=0) == _lib.XK_ERR_INVALID
+
+
+def _mx(**kw):
+    a = dict(A=FAKE, dt=0, M=4, H=64, w13=FAKE, s13=FAKE, w2=FAKE, s2=FAKE, E=2, I=32, b13=None,
+             b2=None, lim=7.0, gs=32, ids=FAKE, w=FAKE, k=2, emap=None, ng=0, mul=1, out=FAKE, ws=FAKE,
+             wsb=1 << 30, stream=None)
+    a.update(kw)
+    return _rc("xk_moe_mxfp4", a["A"], a["dt"], a["M"], a["H"], a["w13"], a["s13"], a["w2"], a["s2"],
+               a["E"], a["I"], a["b13"], a["b2"], a["lim"], a["gs"], a["ids"], a["w"], a["k"],
+               a["emap"], a["ng"], a["mul"], a["out"], a["ws"], a["wsb"], a["stream"])
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(gs=16), _lib.XK_ERR_INVALID), (dict(H=48), _lib.XK_ERR_INVALID),
+    (dict(I=40), _lib.XK_ERR_INVALID), (dict(w2=None), _lib.XK_ERR_INVALID),
+    (dict(dt=-1), _lib.XK_ERR_INVALID), (dict(w=None), _lib.XK_ERR_INVALID),
+    (dict(wsb=100), _lib.XK_ERR_WORKSPACE), (dict(M=0, A=None, out=None), _lib.XK_OK),
+])
+def test_mxfp4_rejects_bad_arguments(kw, code):
+    assert _mx(**kw) == code
+
+
+def test_call_raises_with_message():
+    with pytest.raises(RuntimeError, match="xk_moe_sum_reduce failed"):
+        _lib.call("xk_moe_sum_reduce", FAKE, 7, 4, 2, 8, None, 0, 1.0, FAKE, None)

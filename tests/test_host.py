@@ -1,0 +1,218 @@
+"""Host-side logic of the package without a GPU: backend dispatch (the plugin
+boundary, reference src/xkernels/_dispatch.py:19-247), the registry (schemas,
+arch vocabulary, constraints, cost models, input generators), find_impl
+ranking, and verify / verify_parity behaviour on a CPU-only host (the HIP cards
+must report an error, never silently fall back)."""
+from __future__ import annotations
+
+import json
+
+import pytest
+import torch
+
+import xkernels_amd as xk
+from xkernels_amd import Backend, _dispatch, find_impl, verify, verify_parity
+from xkernels_amd.registry import all_cards, all_specs, get_card, load_shape_sweep
+from xkernels_amd.registry import archs, constraints, cost_model, input_gen, schemas
+
+OPS = ["moe_int4_w4a16@1.0.0", "moe_align_block_size@1.0.0", "moe_sum_reduce@1.0.0",
+       "moe_mxfp4@1.0.0"]
+
+
+# --------------------------------------------------------------- dispatch ----
+
+@pytest.fixture
+def fake_kernel():
+    name = "test_fake_kernel"
+    yield name
+    for b in list(_dispatch.registered_backends(name)):
+        _dispatch.unregister(name, b)
+    _dispatch._BACKEND_FAILURES.pop(name, None)
+
+
+def test_dispatch_explicit_env_and_auto(fake_kernel, monkeypatch):
+    _dispatch.register(fake_kernel, Backend.REFERENCE)(lambda x: ("ref", x))
+    _dispatch.register(fake_kernel, Backend.HIP)(lambda x: ("hip", x))
+    assert _dispatch.dispatch(fake_kernel, 1, backend="reference") == ("ref", 1)
+    assert _dispatch.dispatch(fake_kernel, 2, backend=Backend.HIP) == ("hip", 2)
+    monkeypatch.setenv("XKERNELS_BACKEND", "reference")
+    assert _dispatch.dispatch(fake_kernel, 3) == ("ref", 3)
+    monkeypatch.delenv("XKERNELS_BACKEND")
+    monkeypatch.setattr(_dispatch, "detect_vendor", lambda: "amd")
+    assert _dispatch.select_backend(fake_kernel) is Backend.HIP
+    monkeypatch.setattr(_dispatch, "detect_vendor", lambda: "none")
+    assert _dispatch.select_backend(fake_kernel) is Backend.REFERENCE
+
+
+def test_dispatch_unregistered_backend_raises(fake_kernel, monkeypatch):
+    _dispatch.register(fake_kernel, Backend.REFERENCE)(lambda: 0)
+    with pytest.raises(KeyError, match="not registered"):
+        _dispatch.dispatch(fake_kernel, backend="hip")
+    monkeypatch.setenv("XKERNELS_BACKEND", "hip")
+    with pytest.raises(KeyError):
+        _dispatch.dispatch(fake_kernel)
+    with pytest.raises(KeyError, match="no backends"):
+        _dispatch.dispatch("kernel_nobody_registered")
+
+
+def test_registration_guard_records_and_strict_reraises(fake_kernel, monkeypatch):
+    with _dispatch.backend_registration_guard(fake_kernel, Backend.HIP, source="unit"):
+        raise ImportError("lib missing")
+    diag = _dispatch.backend_diagnostics()
+    assert fake_kernel in diag
+    with pytest.raises(RuntimeError, match="lib missing"):
+        _dispatch.dispatch(fake_kernel)
+    monkeypatch.setenv("XKERNELS_STRICT_BACKENDS", "1")
+    with pytest.raises(ImportError):
+        with _dispatch.backend_registration_guard(fake_kernel, Backend.HIP, source="unit"):
+            raise ImportError("again")
+
+
+def test_reference_fallback_warns_on_gpu_tensors(fake_kernel, monkeypatch):
+    _dispatch.register(fake_kernel, Backend.REFERENCE)(lambda x: x)
+    _dispatch.record_backend_failure(fake_kernel, Backend.HIP, OSError("no .so"), source="unit")
+    monkeypatch.setattr(_dispatch, "detect_vendor", lambda: "amd")
+
+    class FakeCuda:
+        is_cuda = True
+
+    with pytest.warns(RuntimeWarning, match="selected REFERENCE"):
+        _dispatch.dispatch(fake_kernel, FakeCuda())
+
+
+def test_package_registers_hip_for_every_op():
+    for k in ("moe_int4_w4a16", "moe_align_block_size", "moe_sum_reduce", "moe_mxfp4"):
+        assert Backend.HIP in _dispatch.registered_backends(k)
+    assert not any(f for f in _dispatch.backend_failures().values()), _dispatch.backend_diagnostics()
+
+
+def test_hip_ops_refuse_cpu_tensors():
+    A = torch.randn(2, 64).bfloat16()
+    packed, scale, _ = xk.make_w4a16_weights(2, 16, 64, 32, device="cpu", seed=0)
+    ids = torch.zeros(2, 1, dtype=torch.int32)
+    with pytest.raises(RuntimeError, match="device"):
+        xk.fused_moe_int4_w4a16(A, packed, scale, ids, torch.ones(2, 1), backend="hip")
+    with pytest.raises(RuntimeError, match="device"):
+        xk.moe_sum_reduce(torch.randn(2, 2, 8), torch.ones(2, 2), backend="hip")
+    with pytest.raises(RuntimeError, match="device"):
+        xk.moe_align_block_size(ids, 16, 2, backend="hip")
+
+
+# --------------------------------------------------------------- registry ----
+
+def test_every_document_validates():
+    root = schemas.registry_root()
+    for p in sorted((root / "ops").glob("*.json")):
+        schemas.validate_op_spec(json.loads(p.read_text()))
+    for p in sorted((root / "impls").glob("*.json")):
+        schemas.validate_impl_card(json.loads(p.read_text()))
+
+
+def test_validator_rejects_broken_card():
+    doc = json.loads((schemas.registry_root() / "impls" / "moe_int4_w4a16.hip.card.json").read_text())
+    bad = dict(doc)
+    bad.pop("implements")
+    with pytest.raises(Exception):
+        schemas.validate_impl_card(bad)
+    bad = json.loads(json.dumps(doc))
+    bad["arch"]["family"] = "amd_cdna9"
+    with pytest.raises(Exception):
+        schemas.validate_impl_card(bad)
+
+
+def test_arch_vocabulary_matches_schema_enum():
+    enum = schemas.impl_card_schema()
+    text = json.dumps(enum)
+    fam = None
+
+    def walk(n):
+        nonlocal fam
+        if isinstance(n, dict):
+            if "family" in n and isinstance(n["family"], dict) and "enum" in n["family"]:
+                fam = set(n["family"]["enum"])
+            for v in n.values():
+                walk(v)
+        elif isinstance(n, list):
+            for v in n:
+                walk(v)
+
+    walk(enum)
+    assert fam is not None, text[:200]
+    assert fam - {"any"} == set(archs.ALL_ARCHS)
+    assert archs.vendor_of("amd_cdna4") == "amd" and archs.vendor_of("nvidia_sm90") == "nvidia"
+
+
+def test_specs_cards_and_sweeps_load():
+    specs = all_specs()
+    assert set(OPS) <= set(specs)
+    cards = all_cards()
+    for op in OPS:
+        backends = {c.backend.name for c in cards[op].values()}
+        assert {"HIP", "REFERENCE"} <= backends
+        hip = next(c for c in cards[op].values() if c.backend.name == "HIP")
+        assert hip.arch.family == "amd_cdna4"
+        assert len(load_shape_sweep(specs[op].shape_sweep)) >= 1
+        assert input_gen.has_generator(op) and cost_model.has_model(op)
+    assert get_card("moe_int4_w4a16.hip@1.0.0").implements == "moe_int4_w4a16@1.0.0"
+
+
+def test_constraints():
+    assert constraints.evaluate("K % 8 == 0 and N > 0", {"K": 64, "N": 4})
+    assert not constraints.evaluate("K % 8 == 0", {"K": 60})
+    with pytest.raises(constraints.UndecidableConstraintError):
+        constraints.evaluate("K % 8 == 0", {})
+    with pytest.raises(Exception):
+        constraints.validate_decidable("__import__('os')")
+
+
+def test_cost_models_closed_form():
+    # C2 decode: 48 experts x N x K/2 weight bytes + N x K/32 x 2 scale bytes
+    assert cost_model.int4_weight_bytes(48, 4096, 7168) == 792_723_456
+    assert cost_model.mxfp4_expert_bytes(4096, 512) == (2 * 512 * 4096 + 4096 * 512) // 2 \
+        + (2 * 512 * 4096 + 4096 * 512) // 32
+    assert cost_model.arch_peaks("amd_cdna4")["dram_bw_gbs"] == 8000
+
+
+@pytest.mark.parametrize("op", OPS)
+def test_input_generators_are_seeded(op):
+    sweep = all_specs()[op].shape_sweep
+    point = load_shape_sweep(sweep)[0]
+    a = input_gen.generate_inputs(op, point, 7, "cpu")
+    b = input_gen.generate_inputs(op, point, 7, "cpu")
+    for k in a:
+        if isinstance(a[k], torch.Tensor):
+            assert torch.equal(a[k], b[k]), k
+
+
+# ------------------------------------------------------- find_impl, verify ----
+
+def test_find_impl_filters_and_ranks():
+    q = {"A": {"dtype": "bf16", "shape": [64, 7168]}, "packed": {"dtype": "int32", "shape": [48, 4096, 896]}}
+    res = find_impl("gemm", q, target_arch="amd_cdna4", available_features=["matrix_cores", "mfma"])
+    ok = [r for r in res if r["applicable"] and r["op_id"] == "moe_int4_w4a16@1.0.0"]
+    assert ok and ok[0]["backend"] == "HIP"
+    res = find_impl("gemm", q, target_arch="nvidia_sm90")
+    hip = [r for r in res if r["backend"] == "HIP"]
+    assert hip and not hip[0]["applicable"]
+    assert any("nvidia" in x or "family" in x for x in hip[0]["reject_reasons"])
+    bad = {"A": {"dtype": "bf16", "shape": [64, 7170]}, "packed": {"dtype": "int32", "shape": [48, 4096, 896]}}
+    res = find_impl("gemm", bad, target_arch="amd_cdna4", available_features=["matrix_cores", "mfma"])
+    assert all(not r["applicable"] for r in res if r["op_id"] == "moe_int4_w4a16@1.0.0")
+
+
+@pytest.mark.skipif(torch.cuda.is_available(), reason="checks the CPU-only behaviour")
+def test_verify_hip_card_on_cpu_host_reports_error():
+    r = verify("moe_sum_reduce.hip@1.0.0", arch="amd_cdna4")
+    assert r["compiled"] is False and r["correctness"]["passed"] is False
+    assert "device" in r["artifacts"]["error"]
+
+
+def test_verify_reference_card_passes_on_cpu():
+    r = verify("moe_sum_reduce.reference@1.0.0", arch="any")
+    assert r["compiled"] and r["correctness"]["passed"], r
+
+
+@pytest.mark.skipif(torch.cuda.is_available(), reason="checks the CPU-only behaviour")
+def test_verify_parity_on_cpu_is_inconclusive():
+    r = verify_parity("moe_align_block_size@1.0.0", archs=["amd_cdna4"])
+    assert r["inconclusive"] and r["agree"] is None and r["n_runnable"] == 1
