@@ -38,8 +38,15 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--fast-dequant", action="store_true",
                     help="exact (n-8)*s contraction instead of the reference's bf16-rounded weights")
     ap.add_argument("--seed", type=int, default=20)
+    ap.add_argument("--workload", default="c2", choices=["c2", "c3-align", "c3-reduce", "c4", "c5"],
+                    help="c2 is the headline line; the others time the other BASELINE configs' "
+                         "kernels (secondary lines, not the headline metric)")
     ap.add_argument("--profile-only", action="store_true",
                     help="run warmup + timed steps only (for rocprofv3), print nothing else")
+    ap.add_argument("--gemm-only", action="store_true",
+                    help="with --profile-only: launch only the grouped GEMM (for --pmc passes)")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="run 5 device copies of 1 GiB and exit (calibrates FETCH_SIZE/WRITE_SIZE)")
     return ap.parse_args()
 
 
@@ -104,6 +111,143 @@ def time_gemm_kernel(c, flags: int, iters: int) -> float:
     return sum(d) / len(d)
 
 
+COPY_BYTES = 1 << 30
+
+
+def copy_calibration() -> int:
+    """Five plain device-to-device copies of COPY_BYTES: the known-size workload
+    the HBM byte counters are scaled against."""
+    import torch
+
+    src = torch.ones(COPY_BYTES, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    return 0
+
+
+TRAFFIC_FILE = ROOT / "profiles" / "int4_stream_v2_C2_traffic.json"
+
+
+def measured_traffic(exact: bool) -> dict | None:
+    """HBM bytes per GEMM launch from the committed rocprofv3 --pmc summary
+    (FETCH_SIZE and WRITE_SIZE passes, each scaled by the copy calibration)."""
+    try:
+        doc = json.loads(TRAFFIC_FILE.read_text())
+    except (OSError, ValueError):
+        return None
+    entry = doc.get("exact" if exact else "fast")
+    return None if entry is None else entry
+
+
+def _zipf_topk(M: int, top_k: int, E: int, s: float, seed: int):
+    """top_k distinct experts per token, expert popularity Zipf(s) (random rank order)."""
+    import torch
+
+    g = torch.Generator().manual_seed(seed)
+    p = 1.0 / torch.arange(1, E + 1, dtype=torch.float64) ** s
+    probs = torch.zeros(E, dtype=torch.float64)
+    probs[torch.randperm(E, generator=g)] = p / p.sum()
+    return torch.multinomial(probs.expand(M, E), top_k, replacement=False, generator=g).to(torch.int32)
+
+
+def _event_time(fn, steps: int, warmup: int) -> float:
+    """Average ms per call of fn(), HIP events on torch's current stream (the
+    stream the library launches on)."""
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record(stream)
+    for _ in range(steps):
+        fn()
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    return ev0.elapsed_time(ev1) / steps
+
+
+def secondary(a) -> dict:
+    """Time the kernels of BASELINE configs 3-5 (align, sum_reduce, MXFP4, prefill
+    INT4). Each line names its own metric; none replaces the headline."""
+    import torch
+
+    from xkernels_amd import (Backend, fused_moe_int4_w4a16, fused_moe_mxfp4,
+                              make_mxfp4_moe_weights, make_w4a16_weights, moe_align_block_size,
+                              moe_sum_reduce)
+    from xkernels_amd.registry.cost_model import int4_weight_bytes, mxfp4_expert_bytes
+
+    hip = Backend.HIP
+    g = torch.Generator().manual_seed(a.seed)
+    if a.workload == "c3-align":
+        M, k, E, bs = 16384, 8, 48, 16
+        ids = _zipf_topk(M, k, E, 1.1, a.seed).cuda()
+        ms = _event_time(lambda: moe_align_block_size(ids, bs, E, backend=hip), a.steps, a.warmup)
+        numel = M * k
+        max_pad = numel + (E + 1) * (bs - 1)
+        nbytes = numel * 4 + max_pad * 4 + (max_pad // bs) * 4  # ids in, sorted + expert ids out
+        return {"metric": "moe_align_block_size µs at M=16384,top_k=8,E=48,block=16 (Zipf 1.1)",
+                "value": round(ms * 1e3, 2), "unit": "µs", "higher_is_better": False,
+                "config": {"workload": "C3 align"},
+                "roofline": {"bound": "hbm", "achieved": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                             "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                             "frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                             "algorithmic_bytes": nbytes}}
+    if a.workload == "c3-reduce":
+        M, k, H = 8192, 8, 7168
+        y = torch.randn(M, k, H, generator=g).to(torch.bfloat16).cuda()
+        w = torch.softmax(torch.randn(M, k, generator=g), -1).cuda()
+        ms = _event_time(lambda: moe_sum_reduce(y, w, backend=hip), a.steps, a.warmup)
+        nbytes = M * k * H * 2 + M * H * 2 + M * k * 4
+        return {"metric": "moe_sum_reduce µs + GB/s at [8192, 8, 7168] bf16",
+                "value": round(nbytes / (ms * 1e-3) / 1e9, 1), "unit": "GB/s", "higher_is_better": True,
+                "us_per_call": round(ms * 1e3, 2), "config": {"workload": "C3 sum_reduce"},
+                "roofline": {"bound": "hbm", "achieved": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                             "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                             "frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                             "algorithmic_bytes": nbytes}}
+    if a.workload == "c4":
+        M, E, hidden, ispp, k = 48, 256, 4096, 512, 6
+        wts = make_mxfp4_moe_weights(E, hidden, ispp, device="cuda", seed=a.seed, scale_lo=119,
+                                     scale_hi=128)
+        A = torch.randn(M, hidden, generator=g).to(torch.bfloat16).cuda()
+        ids = torch.stack([torch.randperm(E, generator=g)[:k] for _ in range(M)]).to(torch.int32).cuda()
+        w = torch.softmax(torch.randn(M, k, generator=g), -1).cuda()
+        del wts["w13_ref"], wts["w2_ref"]
+        ms = _event_time(lambda: fused_moe_mxfp4(A, wts["w13"], wts["w13_scale"], wts["w2"],
+                                                 wts["w2_scale"], ids, w, backend=hip),
+                         a.steps, a.warmup)
+        e_active = int(torch.unique(ids).numel())
+        nbytes = e_active * mxfp4_expert_bytes(hidden, ispp)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        return {"metric": "moe_mxfp4 µs + HBM GB/s at E=256,hidden=4096,ispp=512,top_k=6,M=48",
+                "value": round(gbs, 1), "unit": "GB/s", "higher_is_better": True,
+                "us_per_call": round(ms * 1e3, 2),
+                "config": {"workload": "C4 mxfp4 decode", "E_active": e_active},
+                "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
+                             "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                             "algorithmic_bytes": nbytes}}
+    # c5: prefill, contraction bound
+    M, E, N, K, k = 4096, 48, 4096, 7168, 8
+    packed, scale, _ = make_w4a16_weights(E, N, K, 32, device="cuda", seed=a.seed, scale_hi=0.02)
+    A = torch.randn(M, K, generator=g).to(torch.bfloat16).cuda()
+    ids = _zipf_topk(M, k, E, 1.2, a.seed).cuda()
+    w = torch.softmax(torch.randn(M, k, generator=g), -1).cuda()
+    ms = _event_time(lambda: fused_moe_int4_w4a16(A, packed, scale, ids, w, backend=hip),
+                     max(1, a.steps // 5), max(1, a.warmup // 5))
+    flops = 2 * M * k * N * K
+    tf = flops / (ms * 1e-3) / 1e12
+    return {"metric": "moe_int4_w4a16 µs + TFLOP/s at M=4096,E=48,N=4096,K=7168,top_k=8 (Zipf 1.2)",
+            "value": round(tf, 1), "unit": "TFLOP/s", "higher_is_better": True,
+            "us_per_call": round(ms * 1e3, 2), "config": {"workload": "C5 int4 prefill"},
+            "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": 2500.0,
+                         "unit": "TFLOP/s", "frac": round(tf / 2500.0, 4), "algorithmic_flops": flops,
+                         "weight_bytes": int4_weight_bytes(E, N, K)}}
+
+
 def cpu_baseline(c) -> dict:
     """The reference backend's literal loop (full dequant of every expert, then one
     fp32 matvec per routed (token, expert)) on the host, on the full C2 batch."""
@@ -152,6 +296,15 @@ def main() -> int:
     if not torch.cuda.is_available():
         print(json.dumps({"error": "no GPU visible"}))
         return 1
+    if a.copy_calibration:
+        return copy_calibration()
+    if a.workload != "c2":
+        line = secondary(a)
+        line.update({"n_gpus": 1, "steps": a.steps, "warmup": a.warmup, "dtype": "bf16",
+                     "data": "synthetic (seeded)", "secondary": True})
+        if not a.profile_only:
+            print(json.dumps(line))
+        return 0
     c = make_inputs(a.seed)
     exact = not a.fast_dequant
     flags = 0 if exact else _lib.XK_INT4_FAST_DEQUANT
@@ -168,6 +321,9 @@ def main() -> int:
         return moe_int4_w4a16_hip(c["A"], c["packed"], c["scale"], c["ids"], c["w"],
                                   workspace=ws, exact_dequant=False)
 
+    if a.profile_only and a.gemm_only:
+        time_gemm_kernel(c, flags, a.steps)
+        return 0
     for _ in range(a.warmup):
         step()
     torch.cuda.synchronize()
@@ -206,12 +362,18 @@ def main() -> int:
                    "E_active": e_active, "weight_scale_bytes": weight_bytes,
                    "dequant": "bf16-rounded (reference)" if exact else "exact fp32 (fast)",
                    "wall_s_timed_region": round(wall, 4)},
-        "roofline": {"bound": "hbm", "kernel": "int4_stream_gemm_rne" if exact else "int4_stream_gemm",
+        "roofline": {"bound": "hbm",
+                     "kernel": "int4_stream_v2<Int4Mode::%s>" % ("kRne" if exact else "kFast"),
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "avg_launch_us": round(gemm_ms * 1e3, 2),
+                     "avg_launch_us": round(gemm_ms * 1e3, 3),
+                     "algorithmic_bytes": weight_bytes,
                      "traffic": None},
     }
+    t = measured_traffic(exact)
+    if t is not None:
+        line["roofline"]["traffic"] = t["bytes_per_launch"]
+        line["roofline"]["traffic_source"] = str(TRAFFIC_FILE.relative_to(ROOT))
     if not a.no_cpu:
         line["cpu_baseline"] = cpu_baseline(c)
     print(json.dumps(line))
