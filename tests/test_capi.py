@@ -37,7 +37,8 @@ def test_library_exports_every_declared_symbol():
 def test_constants_match_header():
     d = _defines()
     for name in ("XK_OK", "XK_ERR_INVALID", "XK_ERR_WORKSPACE", "XK_ERR_LAUNCH", "XK_DT_BF16",
-                 "XK_DT_FP32", "XK_DT_NONE", "XK_INT4_FAST_DEQUANT", "XK_INT4_V1"):
+                 "XK_DT_FP32", "XK_DT_NONE", "XK_INT4_FAST_DEQUANT", "XK_INT4_V1",
+                 "XK_INT4_FORCE_TILE", "XK_INT4_FORCE_STREAM"):
         assert getattr(_lib, name) == d[name], name
 
 

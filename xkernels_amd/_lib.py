@@ -22,6 +22,8 @@ XK_DT_FP32 = 1
 XK_DT_NONE = -1
 XK_INT4_FAST_DEQUANT = 1
 XK_INT4_V1 = 2
+XK_INT4_FORCE_TILE = 4
+XK_INT4_FORCE_STREAM = 8
 
 _p = ctypes.c_void_p
 _i32 = ctypes.c_int32

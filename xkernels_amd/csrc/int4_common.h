@@ -1,0 +1,61 @@
+// Device helpers shared by the INT4 GEMM kernels (decode stream and prefill tile).
+#pragma once
+
+#include "common.h"
+
+namespace xk {
+
+// Reorders 8 consecutive bf16 (4 dwords a0a1 a2a3 a4a5 a6a7) into the order
+// the nibble unpack yields: a0a4 a1a5 a2a6 a3a7.
+__device__ __forceinline__ void perm8(const uint32_t* in, uint32_t* o) {
+  o[0] = (in[0] & 0xFFFFu) | (in[2] << 16);
+  o[1] = (in[0] >> 16) | (in[2] & 0xFFFF0000u);
+  o[2] = (in[1] & 0xFFFFu) | (in[3] << 16);
+  o[3] = (in[1] >> 16) | (in[3] & 0xFFFF0000u);
+}
+
+// 4x4 transpose of 32-bit words across the four 16-lane groups:
+// out[j] in lane group q = in[q] of lane group j.
+__device__ __forceinline__ void transpose4(u32x4& w) {
+  auto a = __builtin_amdgcn_permlane32_swap(w[0], w[2], false, false);
+  auto b = __builtin_amdgcn_permlane32_swap(w[1], w[3], false, false);
+  auto c = __builtin_amdgcn_permlane16_swap(a[0], b[0], false, false);
+  auto d = __builtin_amdgcn_permlane16_swap(a[1], b[1], false, false);
+  w = u32x4{c[0], c[1], d[0], d[1]};
+}
+
+// (x & m) | k in one v_and_or_b32 (the compiler otherwise splits it in two).
+__device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t m, uint32_t k) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "v"(m), "v"(k));
+  return r;
+}
+
+// 8 nibbles of `w` (low nibble = lowest k) -> 8 bf16 = bf16_rne((n - 8) * s),
+// the reference's dequant rounding. Each nibble pair becomes two fp16 values
+// 1024 + n (one v_and_or_b32); v_fma_mix_f32 forms (1024 + n) * s - 1032 * s
+// exactly in fp32 (both terms fit 24 bits), and v_cvt_pk_bf16_f32 rounds.
+// Output element order: n0 n4 n1 n5 n2 n6 n3 n7 (pairs d, d + 4).
+__device__ __forceinline__ bf16x8 dequant_rne(uint32_t w, float s, float ms1032, uint32_t mask) {
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  typedef float f2 __attribute__((ext_vector_type(2)));
+  typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+  u32x4 b;
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    const h2 x = __builtin_bit_cast(h2, and_or(w >> (4 * d), mask, 0x64006400u));
+    const f2 v = {fmaf(static_cast<float>(x[0]), s, ms1032), fmaf(static_cast<float>(x[1]), s, ms1032)};
+    b[d] = __builtin_bit_cast(uint32_t, __builtin_convertvector(v, b2));
+  }
+  return __builtin_bit_cast(bf16x8, b);
+}
+
+// 8 nibbles -> bf16 (128 + n), same element order as dequant_rne.
+__device__ __forceinline__ bf16x8 dequant_magic(uint32_t w, uint32_t mask) {
+  u32x4 b;
+#pragma unroll
+  for (int d = 0; d < 4; ++d) b[d] = and_or(w >> (4 * d), mask, 0x43004300u);
+  return __builtin_bit_cast(bf16x8, b);
+}
+
+}  // namespace xk

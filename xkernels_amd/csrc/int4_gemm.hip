@@ -34,7 +34,7 @@
 // fp32 sweep points and unusual group sizes.
 #include <algorithm>
 
-#include "common.h"
+#include "int4_common.h"
 
 namespace xk {
 namespace {
@@ -63,14 +63,6 @@ __device__ __forceinline__ uint32_t nib_pair(uint32_t w, int shift) {
   return ((w >> shift) & 0x000F000Fu) | 0x43004300u;
 }
 
-// Reorders 8 consecutive bf16 (4 dwords a0a1 a2a3 a4a5 a6a7) into the order
-// the nibble unpack yields: a0a4 a1a5 a2a6 a3a7.
-__device__ __forceinline__ void perm8(const uint32_t* in, uint32_t* o) {
-  o[0] = (in[0] & 0xFFFFu) | (in[2] << 16);
-  o[1] = (in[0] >> 16) | (in[2] & 0xFFFF0000u);
-  o[2] = (in[1] & 0xFFFFu) | (in[3] << 16);
-  o[3] = (in[1] >> 16) | (in[3] & 0xFFFF0000u);
-}
 
 __global__ void __launch_bounds__(256)
 int4_stream_gemm(StreamArgs p) {
@@ -474,50 +466,6 @@ __device__ __forceinline__ int count_active_experts(const int32_t* offsets, int 
   return n;
 }
 
-// 4x4 transpose of 32-bit words across the four 16-lane groups:
-// out[j] in lane group q = in[q] of lane group j.
-__device__ __forceinline__ void transpose4(u32x4& w) {
-  auto a = __builtin_amdgcn_permlane32_swap(w[0], w[2], false, false);
-  auto b = __builtin_amdgcn_permlane32_swap(w[1], w[3], false, false);
-  auto c = __builtin_amdgcn_permlane16_swap(a[0], b[0], false, false);
-  auto d = __builtin_amdgcn_permlane16_swap(a[1], b[1], false, false);
-  w = u32x4{c[0], c[1], d[0], d[1]};
-}
-
-// (x & m) | k in one v_and_or_b32 (the compiler otherwise splits it in two).
-__device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t m, uint32_t k) {
-  uint32_t r;
-  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "v"(m), "v"(k));
-  return r;
-}
-
-// 8 nibbles of `w` (low nibble = lowest k) -> 8 bf16 = bf16_rne((n - 8) * s),
-// the reference's dequant rounding. Each nibble pair becomes two fp16 values
-// 1024 + n (one v_and_or_b32); v_fma_mix_f32 forms (1024 + n) * s - 1032 * s
-// exactly in fp32 (both terms fit 24 bits), and v_cvt_pk_bf16_f32 rounds.
-// Output element order: n0 n4 n1 n5 n2 n6 n3 n7 (pairs d, d + 4).
-__device__ __forceinline__ bf16x8 dequant_rne(uint32_t w, float s, float ms1032, uint32_t mask) {
-  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-  typedef float f2 __attribute__((ext_vector_type(2)));
-  typedef __bf16 b2 __attribute__((ext_vector_type(2)));
-  u32x4 b;
-#pragma unroll
-  for (int d = 0; d < 4; ++d) {
-    const h2 x = __builtin_bit_cast(h2, and_or(w >> (4 * d), mask, 0x64006400u));
-    const f2 v = {fmaf(static_cast<float>(x[0]), s, ms1032), fmaf(static_cast<float>(x[1]), s, ms1032)};
-    b[d] = __builtin_bit_cast(uint32_t, __builtin_convertvector(v, b2));
-  }
-  return __builtin_bit_cast(bf16x8, b);
-}
-
-// 8 nibbles -> bf16 (128 + n), same element order as dequant_rne.
-__device__ __forceinline__ bf16x8 dequant_magic(uint32_t w, uint32_t mask) {
-  u32x4 b;
-#pragma unroll
-  for (int d = 0; d < 4; ++d) b[d] = and_or(w >> (4 * d), mask, 0x43004300u);
-  return __builtin_bit_cast(bf16x8, b);
-}
-
 template <Int4Mode MODE>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 int4_stream_v2(V2Args args) {
@@ -745,18 +693,6 @@ int4_stream_v2(V2Args args) {
   }
 }
 
-int device_cu_count() {
-  static int cached[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cached[dev] == 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
-      n = 256;
-    cached[dev] = n;
-  }
-  return cached[dev];
-}
 
 // One thread per (slot, column); exact dequant rounded to A's dtype.
 template <typename TA>
@@ -793,6 +729,20 @@ int4_simple_gemm(const TA* __restrict__ A, int K, const uint32_t* __restrict__ p
 
 }  // namespace
 
+// Number of compute units of the current device (cached per device).
+int device_cu_count() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
 // Token-slot block size the stream kernel consumes (one MFMA row tile).
 int int4_block_size() { return 16; }
 
@@ -806,6 +756,16 @@ int int4_gemm_parts(int64_t E, int64_t N, int64_t K, int a_dtype, int group_size
   (void)E; (void)N; (void)K; (void)a_dtype; (void)group_size; (void)flags;
   return 1;
 }
+
+bool int4_prefill_ok(int a_dtype, int group_size, int64_t K, int64_t N, int64_t E);
+int launch_int4_prefill(const void* A, int64_t K, const int32_t* packed, const uint16_t* scale,
+                        int64_t E, int64_t N, int64_t numel, int64_t top_k,
+                        const int32_t* sorted_ids, const int32_t* offsets, float* slot_out,
+                        hipStream_t stream);
+
+// Routed rows per expert (on average) from which the tile kernel replaces the
+// weight-streaming kernel.
+constexpr int64_t kPrefillRowsPerExpert = 64;
 
 int launch_int4_gemm(const void* A, int a_dtype, int64_t M, int64_t K, const int32_t* packed,
                      const uint16_t* scale, int64_t E, int64_t N, int group_size,
@@ -824,6 +784,13 @@ int launch_int4_gemm(const void* A, int a_dtype, int64_t M, int64_t K, const int
   if (int4_use_stream(a_dtype, group_size, K)) {
     XK_REQUIRE(sorted_ids && offsets, "int4: stream kernel needs align outputs");
     XK_REQUIRE(reinterpret_cast<uintptr_t>(A) % 16 == 0, "int4: A must be 16-byte aligned");
+    const bool tile_ok = int4_prefill_ok(a_dtype, group_size, K, N, E) &&
+                         reinterpret_cast<uintptr_t>(packed) % 16 == 0;
+    const bool want_tile = (flags & XK_INT4_FORCE_TILE) ||
+                           (numel >= kPrefillRowsPerExpert * E && !(flags & XK_INT4_FORCE_STREAM));
+    if (tile_ok && want_tile && !(flags & XK_INT4_V1))
+      return launch_int4_prefill(A, K, packed, scale, E, N, numel, top_k, sorted_ids, offsets,
+                                 slot_out, stream);
     StreamArgs a{static_cast<const uint16_t*>(A), reinterpret_cast<const uint32_t*>(packed),
                  scale, sorted_ids, offsets, slot_out, int(K), int(N), int(numel), int(top_k),
                  int((K / 32) % 8 == 0 && reinterpret_cast<uintptr_t>(scale) % 16 == 0)};

@@ -1,0 +1,256 @@
+// Prefill-regime grouped INT4 W4A16 MoE GEMM for gfx950 (the reference's
+// _fused_moe_int4_kernel at large M, src/xkernels/ops/moe/triton/moe_int4_kernel.py:78-272;
+// math of reference.py:22-70 with the dequant of w4a16.py:21-50).
+//
+// Same contract as the decode stream kernel: for every routed slot t of local
+// expert e it writes the un-weighted fp32 row
+//   slot_out[t, n] = sum_k A[t / top_k, k] * bf16((nibble(e, n, k) - 8) * scale[e, n, k / 32])
+// and the weighted top-k combine runs afterwards.
+//
+// With hundreds of routed rows per expert the work is contraction bound, so the
+// kernel is an MFMA tile GEMM:
+//   * a tile is (expert e, 128 consecutive rows of e's padded slot range, 256
+//     output columns); tiles are enumerated on the device from the align
+//     offsets, so no host synchronisation is needed;
+//   * a persistent grid (one workgroup per CU) walks the tiles; tiles are cut
+//     into 8 contiguous ranges, one per XCD (workgroup b runs on XCD b % 8), and
+//     the column blocks of one row block are adjacent in a range, so the
+//     workgroups running together on an XCD share the row block's activations
+//     in that XCD's L2;
+//   * 8 waves = 2 row halves x 4 column quarters; each wave owns 64 x 64 outputs
+//     (4 x 4 tiles of v_mfma_f32_16x16x32_bf16) in 64 accumulator registers;
+//   * per 128-k step the 128 gathered activation rows are staged in LDS (double
+//     buffered, 272-byte row stride: the 16-byte MFMA operand reads of 16 rows
+//     hit distinct bank groups), k-permuted within each 8-group to the order the
+//     nibble unpack yields;
+//   * lane (c, q) of a wave loads 16 bytes = 32 k of its weight row (quantisation
+//     group q of the step) directly into registers, two steps ahead, and
+//     dequantises each word with the same fp16-magic / fma_mix / RNE sequence as
+//     the decode kernel, which reproduces the reference's bf16-rounded weights
+//     bit for bit.
+#include <algorithm>
+
+#include "int4_common.h"
+
+namespace xk {
+namespace {
+
+constexpr int kPBM = 128;              // routed rows per tile
+constexpr int kPBN = 256;              // output columns per tile
+constexpr int kPBK = 128;              // k per pipeline step (4 quantisation groups)
+constexpr int kPWaves = 8;             // 2 row halves x 4 column quarters
+constexpr int kPThreads = kPWaves * 64;
+constexpr int kPStride = kPBK + 8;     // bf16 per LDS row (68 dwords)
+constexpr int kPMaxExperts = 1024;
+constexpr int kXcds = 8;               // MI355X: 8 XCDs, workgroups round-robin over them
+
+struct PrefillArgs {
+  const uint16_t* A;       // [M, K] bf16
+  const uint32_t* packed;  // [E, N, K/8]
+  const uint16_t* scale;   // [E, N, K/32] bf16
+  const int32_t* sorted_ids;
+  const int32_t* offsets;  // [E+1] padded slot prefix
+  float* out;              // [numel, N]
+  int K, N, numel, top_k, num_experts;
+};
+
+__global__ void __launch_bounds__(kPThreads)
+int4_prefill_gemm(PrefillArgs p) {
+  __shared__ __attribute__((aligned(16))) uint16_t a_lds[2][kPBM * kPStride];
+  __shared__ int tok_lds[kPBM];
+  __shared__ int slot_lds[kPBM];
+  __shared__ int mt_prefix[kPMaxExperts + 1];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int c16 = lane & 15, q = lane >> 4;
+  const int wm = wave & 1, wn = wave >> 1;
+  const int K = p.K, N = p.N, KW = K >> 3, G = K >> 5;
+  const int steps = K / kPBK;
+  const int NB = N / kPBN;
+  const int E = p.num_experts;
+  const uint32_t kNibMask = 0x000F000Fu;
+
+  // Row blocks per expert, as an inclusive prefix (wave 0, 64 experts a round).
+  if (wave == 0) {
+    int run = 0;
+    for (int base = 0; base < E; base += 64) {
+      const int e = base + lane;
+      int x = e < E ? (p.offsets[e + 1] - p.offsets[e] + kPBM - 1) / kPBM : 0;
+#pragma unroll
+      for (int d = 1; d < 64; d <<= 1) {
+        const int y = __shfl_up(x, d);
+        if (lane >= d) x += y;
+      }
+      if (e < E) mt_prefix[e + 1] = run + x;
+      run += __shfl(x, 63);
+    }
+    if (lane == 0) mt_prefix[0] = 0;
+  }
+  __syncthreads();
+  const int T = mt_prefix[E] * NB;
+  const int xcd = blockIdx.x % kXcds, idx = blockIdx.x / kXcds;
+  const int per_xcd = gridDim.x / kXcds;
+  const int t_beg = static_cast<int>(static_cast<int64_t>(T) * xcd / kXcds);
+  const int t_end = static_cast<int>(static_cast<int64_t>(T) * (xcd + 1) / kXcds);
+
+  const int st_row = tid >> 4, st_kv = tid & 15;  // A staging: rows st_row + 32 i, 8 k at st_kv
+
+  for (int t = t_beg + idx; t < t_end; t += per_xcd) {
+    const int mtile = t / NB, nb = t - mtile * NB;
+    int lo = 0, hi = E;  // mt_prefix[lo] <= mtile < mt_prefix[hi]
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (mt_prefix[mid] <= mtile) lo = mid; else hi = mid;
+    }
+    const int e = lo;
+    const int row0 = p.offsets[e] + (mtile - mt_prefix[e]) * kPBM;
+    const int rows = min(kPBM, p.offsets[e + 1] - row0);
+    const int n0 = nb * kPBN + wn * 64;
+
+    __syncthreads();  // the previous tile is done with slot_lds / a_lds
+    if (tid < kPBM) {
+      int slot = -1, tok = -1;
+      if (tid < rows) {
+        const int s = p.sorted_ids[row0 + tid];
+        if (s < p.numel) { slot = s; tok = s / p.top_k; }
+      }
+      slot_lds[tid] = slot;
+      tok_lds[tid] = tok;
+    }
+    __syncthreads();
+
+    // Rows without a token read token 0: MFMA rows are independent and those
+    // rows are never stored, so every load stays unconditional.
+    const u32x4* a_src[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int tok = max(tok_lds[st_row + 32 * i], 0);
+      a_src[i] = reinterpret_cast<const u32x4*>(p.A + static_cast<int64_t>(tok) * K) + st_kv;
+    }
+    const u32x4* wrow[4];
+    const uint16_t* srow[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int64_t n = static_cast<int64_t>(e) * N + n0 + 16 * c + c16;
+      wrow[c] = reinterpret_cast<const u32x4*>(p.packed + n * KW) + q;
+      srow[c] = p.scale + n * G + q;
+    }
+
+    auto load_a = [&](int s, u32x4 (&ar)[4]) {
+      s = min(s, steps - 1);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) ar[i] = a_src[i][s * (kPBK / 8)];
+    };
+    auto store_a = [&](int buf, const u32x4 (&ar)[4]) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t in[4] = {ar[i][0], ar[i][1], ar[i][2], ar[i][3]};
+        uint32_t o[4];
+        perm8(in, o);
+        *reinterpret_cast<u32x4*>(&a_lds[buf][(st_row + 32 * i) * kPStride + st_kv * 8]) =
+            u32x4{o[0], o[1], o[2], o[3]};
+      }
+    };
+    auto load_w = [&](int s, u32x4 (&w)[4], uint32_t (&sv)[4]) {
+      s = min(s, steps - 1);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        w[c] = wrow[c][s * (kPBK / 32)];
+        sv[c] = srow[c][s * (kPBK / 32)];
+      }
+    };
+
+    f32x4 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) acc[i][c] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    auto compute = [&](int buf, const u32x4 (&w)[4], const uint32_t (&sv)[4]) {
+      float s[4], ms[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        s[c] = __uint_as_float(sv[c] << 16);
+        ms[c] = -1032.0f * s[c];
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        bf16x8 af[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          af[i] = *reinterpret_cast<const bf16x8*>(
+              &a_lds[buf][(wm * 64 + i * 16 + c16) * kPStride + q * 32 + j * 8]);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const bf16x8 b = dequant_rne(w[c][j], s[c], ms[c], kNibMask);
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            acc[i][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], b, acc[i][c], 0, 0, 0);
+        }
+      }
+    };
+
+    u32x4 ar[4], w0[4], w1[4];
+    uint32_t s0[4], s1[4];
+    load_w(0, w0, s0);
+    load_w(1, w1, s1);
+    load_a(0, ar);
+    store_a(0, ar);
+    load_a(1, ar);
+    // step s: A(s+1) -> LDS buffer (s+1)&1 (freed by compute(s-1)); request
+    // A(s+2); contract step s; refill the consumed weight registers with
+    // W(s+2), so a weight load is two steps old when it is used.
+    auto step = [&](int s, u32x4 (&w)[4], uint32_t (&sv)[4]) {
+      __syncthreads();
+      store_a((s + 1) & 1, ar);
+      load_a(s + 2, ar);
+      __builtin_amdgcn_sched_barrier(0);
+      compute(s & 1, w, sv);
+      load_w(s + 2, w, sv);
+    };
+    for (int s = 0; s < steps; s += 2) {
+      step(s, w0, s0);
+      step(s + 1, w1, s1);
+    }
+
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int slot = slot_lds[wm * 64 + i * 16 + q * 4 + v];
+        if (slot < 0) continue;
+        float* orow = p.out + static_cast<int64_t>(slot) * N + n0 + c16;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) orow[16 * c] = acc[i][c][v];
+      }
+  }
+}
+
+}  // namespace
+
+int device_cu_count();
+
+// Shapes the tile kernel takes: bf16 activations, group 32, K a multiple of two
+// steps, N a multiple of the column tile, at most kPMaxExperts local experts.
+bool int4_prefill_ok(int a_dtype, int group_size, int64_t K, int64_t N, int64_t E) {
+  return a_dtype == XK_DT_BF16 && group_size == 32 && K % (2 * kPBK) == 0 && N % kPBN == 0 &&
+         E <= kPMaxExperts;
+}
+
+int launch_int4_prefill(const void* A, int64_t K, const int32_t* packed, const uint16_t* scale,
+                        int64_t E, int64_t N, int64_t numel, int64_t top_k,
+                        const int32_t* sorted_ids, const int32_t* offsets, float* slot_out,
+                        hipStream_t stream) {
+  XK_REQUIRE(reinterpret_cast<uintptr_t>(A) % 16 == 0 && reinterpret_cast<uintptr_t>(packed) % 16 == 0,
+             "int4 prefill: A and packed must be 16-byte aligned");
+  PrefillArgs a{static_cast<const uint16_t*>(A), reinterpret_cast<const uint32_t*>(packed), scale,
+                sorted_ids, offsets, slot_out, int(K), int(N), int(numel), int(top_k), int(E)};
+  // one workgroup per CU, a multiple of the XCD count
+  const int cus = device_cu_count();
+  const int grid = std::max(kXcds, cus / kXcds * kXcds);
+  hipLaunchKernelGGL(int4_prefill_gemm, dim3(grid), dim3(kPThreads), 0, stream, a);
+  XK_CHECK_LAUNCH("int4_prefill_gemm");
+  return XK_OK;
+}
+
+}  // namespace xk
