@@ -17,12 +17,16 @@
 //     the column blocks of one row block are adjacent in a range, so the
 //     workgroups running together on an XCD share the row block's activations
 //     in that XCD's L2;
-//   * 8 waves = 2 row halves x 4 column quarters; each wave owns 64 x 64 outputs
-//     (4 x 4 tiles of v_mfma_f32_16x16x32_bf16) in 64 accumulator registers;
+//   * 8 waves split the 256 columns; each wave owns all 128 rows x 32 columns
+//     (8 x 2 tiles of v_mfma_f32_16x16x32_bf16, 64 accumulator registers), so
+//     every weight is dequantised by exactly one wave;
 //   * per 128-k step the 128 gathered activation rows are staged in LDS (double
-//     buffered, 272-byte row stride: the 16-byte MFMA operand reads of 16 rows
-//     hit distinct bank groups), k-permuted within each 8-group to the order the
-//     nibble unpack yields;
+//     buffered), k-permuted within each 8-group to the order the nibble unpack
+//     yields. gfx950 serves a 16-byte LDS read for 32 lanes at a time from 128
+//     banks, so the 32 lanes (16 rows x 2 lane groups) of one read must hit 32
+//     distinct 16-byte bank groups: rows are 288 bytes apart (18 groups) and the
+//     16-byte chunk (lane group q, MFMA j) of a row sits at chunk 4j + q, which
+//     makes those 32 groups distinct (measured conflict-free);
 //   * lane (c, q) of a wave loads 16 bytes = 32 k of its weight row (quantisation
 //     group q of the step) directly into registers, two steps ahead, and
 //     dequantises each word with the same fp16-magic / fma_mix / RNE sequence as
@@ -38,9 +42,13 @@ namespace {
 constexpr int kPBM = 128;              // routed rows per tile
 constexpr int kPBN = 256;              // output columns per tile
 constexpr int kPBK = 128;              // k per pipeline step (4 quantisation groups)
-constexpr int kPWaves = 8;             // 2 row halves x 4 column quarters
+constexpr int kWM = 1;                 // waves along the rows
+constexpr int kWN = 8;                 // waves along the columns
+constexpr int kPWaves = kWM * kWN;
 constexpr int kPThreads = kPWaves * 64;
-constexpr int kPStride = kPBK + 8;     // bf16 per LDS row (68 dwords)
+constexpr int kRT = kPBM / kWM / 16;   // 16-row MFMA tiles per wave
+constexpr int kCT = kPBN / kWN / 16;   // 16-column MFMA tiles per wave
+constexpr int kPStride = kPBK + 16;    // bf16 per LDS row (72 dwords)
 constexpr int kPMaxExperts = 1024;
 constexpr int kXcds = 8;               // MI355X: 8 XCDs, workgroups round-robin over them
 
@@ -63,7 +71,7 @@ int4_prefill_gemm(PrefillArgs p) {
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int c16 = lane & 15, q = lane >> 4;
-  const int wm = wave & 1, wn = wave >> 1;
+  const int wm = wave % kWM, wn = wave / kWM;
   const int K = p.K, N = p.N, KW = K >> 3, G = K >> 5;
   const int steps = K / kPBK;
   const int NB = N / kPBN;
@@ -93,7 +101,11 @@ int4_prefill_gemm(PrefillArgs p) {
   const int t_beg = static_cast<int>(static_cast<int64_t>(T) * xcd / kXcds);
   const int t_end = static_cast<int>(static_cast<int64_t>(T) * (xcd + 1) / kXcds);
 
-  const int st_row = tid >> 4, st_kv = tid & 15;  // A staging: rows st_row + 32 i, 8 k at st_kv
+  // A staging: thread -> (row st_row + 32 i, 16-byte chunk st_kv). The two
+  // 16-lane halves of each 32-lane LDS write group take rows 8 apart, whose
+  // bank groups are disjoint.
+  const int st_kv = tid & 15, st_g = tid >> 4;
+  const int st_row = (st_g & 1) * 8 + ((st_g >> 1) & 7) + 16 * (st_g >> 4);
 
   for (int t = t_beg + idx; t < t_end; t += per_xcd) {
     const int mtile = t / NB, nb = t - mtile * NB;
@@ -105,7 +117,7 @@ int4_prefill_gemm(PrefillArgs p) {
     const int e = lo;
     const int row0 = p.offsets[e] + (mtile - mt_prefix[e]) * kPBM;
     const int rows = min(kPBM, p.offsets[e + 1] - row0);
-    const int n0 = nb * kPBN + wn * 64;
+    const int n0 = nb * kPBN + wn * (kCT * 16);
 
     __syncthreads();  // the previous tile is done with slot_lds / a_lds
     if (tid < kPBM) {
@@ -127,10 +139,10 @@ int4_prefill_gemm(PrefillArgs p) {
       const int tok = max(tok_lds[st_row + 32 * i], 0);
       a_src[i] = reinterpret_cast<const u32x4*>(p.A + static_cast<int64_t>(tok) * K) + st_kv;
     }
-    const u32x4* wrow[4];
-    const uint16_t* srow[4];
+    const u32x4* wrow[kCT];
+    const uint16_t* srow[kCT];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
+    for (int c = 0; c < kCT; ++c) {
       const int64_t n = static_cast<int64_t>(e) * N + n0 + 16 * c + c16;
       wrow[c] = reinterpret_cast<const u32x4*>(p.packed + n * KW) + q;
       srow[c] = p.scale + n * G + q;
@@ -147,51 +159,53 @@ int4_prefill_gemm(PrefillArgs p) {
         const uint32_t in[4] = {ar[i][0], ar[i][1], ar[i][2], ar[i][3]};
         uint32_t o[4];
         perm8(in, o);
-        *reinterpret_cast<u32x4*>(&a_lds[buf][(st_row + 32 * i) * kPStride + st_kv * 8]) =
+        // global chunk st_kv = 4 q + j goes to chunk 4 j + q
+        *reinterpret_cast<u32x4*>(
+            &a_lds[buf][(st_row + 32 * i) * kPStride + ((st_kv & 3) * 4 + (st_kv >> 2)) * 8]) =
             u32x4{o[0], o[1], o[2], o[3]};
       }
     };
-    auto load_w = [&](int s, u32x4 (&w)[4], uint32_t (&sv)[4]) {
+    auto load_w = [&](int s, u32x4 (&w)[kCT], uint32_t (&sv)[kCT]) {
       s = min(s, steps - 1);
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
+      for (int c = 0; c < kCT; ++c) {
         w[c] = wrow[c][s * (kPBK / 32)];
         sv[c] = srow[c][s * (kPBK / 32)];
       }
     };
 
-    f32x4 acc[4][4];
+    f32x4 acc[kRT][kCT];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < kRT; ++i)
 #pragma unroll
-      for (int c = 0; c < 4; ++c) acc[i][c] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int c = 0; c < kCT; ++c) acc[i][c] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    auto compute = [&](int buf, const u32x4 (&w)[4], const uint32_t (&sv)[4]) {
-      float s[4], ms[4];
+    auto compute = [&](int buf, const u32x4 (&w)[kCT], const uint32_t (&sv)[kCT]) {
+      float s[kCT], ms[kCT];
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
+      for (int c = 0; c < kCT; ++c) {
         s[c] = __uint_as_float(sv[c] << 16);
         ms[c] = -1032.0f * s[c];
       }
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        bf16x8 af[4];
+        bf16x8 af[kRT];
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < kRT; ++i)
           af[i] = *reinterpret_cast<const bf16x8*>(
-              &a_lds[buf][(wm * 64 + i * 16 + c16) * kPStride + q * 32 + j * 8]);
+              &a_lds[buf][(wm * kRT * 16 + i * 16 + c16) * kPStride + (j * 4 + q) * 8]);
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
+        for (int c = 0; c < kCT; ++c) {
           const bf16x8 b = dequant_rne(w[c][j], s[c], ms[c], kNibMask);
 #pragma unroll
-          for (int i = 0; i < 4; ++i)
+          for (int i = 0; i < kRT; ++i)
             acc[i][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], b, acc[i][c], 0, 0, 0);
         }
       }
     };
 
-    u32x4 ar[4], w0[4], w1[4];
-    uint32_t s0[4], s1[4];
+    u32x4 ar[4], w0[kCT], w1[kCT];
+    uint32_t s0[kCT], s1[kCT];
     load_w(0, w0, s0);
     load_w(1, w1, s1);
     load_a(0, ar);
@@ -200,12 +214,16 @@ int4_prefill_gemm(PrefillArgs p) {
     // step s: A(s+1) -> LDS buffer (s+1)&1 (freed by compute(s-1)); request
     // A(s+2); contract step s; refill the consumed weight registers with
     // W(s+2), so a weight load is two steps old when it is used.
-    auto step = [&](int s, u32x4 (&w)[4], uint32_t (&sv)[4]) {
+    // (scheduling barriers keep the compiler from sinking the activation loads
+    // to their use or hoisting the next store's permutes into compute(), either
+    // of which would make a step wait for loads issued in the same step)
+    auto step = [&](int s, u32x4 (&w)[kCT], uint32_t (&sv)[kCT]) {
       __syncthreads();
       store_a((s + 1) & 1, ar);
       load_a(s + 2, ar);
       __builtin_amdgcn_sched_barrier(0);
       compute(s & 1, w, sv);
+      __builtin_amdgcn_sched_barrier(0);
       load_w(s + 2, w, sv);
     };
     for (int s = 0; s < steps; s += 2) {
@@ -214,14 +232,14 @@ int4_prefill_gemm(PrefillArgs p) {
     }
 
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < kRT; ++i)
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        const int slot = slot_lds[wm * 64 + i * 16 + q * 4 + v];
+        const int slot = slot_lds[wm * kRT * 16 + i * 16 + q * 4 + v];
         if (slot < 0) continue;
         float* orow = p.out + static_cast<int64_t>(slot) * N + n0 + c16;
 #pragma unroll
-        for (int c = 0; c < 4; ++c) orow[16 * c] = acc[i][c][v];
+        for (int c = 0; c < kCT; ++c) orow[16 * c] = acc[i][c][v];
       }
   }
 }
