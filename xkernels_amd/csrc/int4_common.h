@@ -24,11 +24,19 @@ __device__ __forceinline__ void transpose4(u32x4& w) {
   w = u32x4{c[0], c[1], d[0], d[1]};
 }
 
-// (x & m) | k in one v_and_or_b32 (the compiler otherwise splits it in two).
-__device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t m, uint32_t k) {
+// A wave-uniform constant held in a VGPR. A VOP3 instruction may read at most one
+// SGPR or literal on gfx950, so with the nibble mask in a VGPR the compiler
+// selects one v_and_or_b32 for (x & mask) | k instead of v_and_b32 + v_or_b32,
+// and the unpack stays plain code the scheduler can interleave with MFMAs.
+__device__ __forceinline__ uint32_t in_vgpr(uint32_t x) {
   uint32_t r;
-  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "v"(m), "v"(k));
+  asm volatile("v_mov_b32 %0, %1" : "=v"(r) : "s"(x));
   return r;
+}
+
+// (x & m) | k with k & m == 0 (one v_and_or_b32 when m is in a VGPR).
+__device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t m, uint32_t k) {
+  return (x & m) | k;
 }
 
 // 8 nibbles of `w` (low nibble = lowest k) -> 8 bf16 = bf16_rne((n - 8) * s),

@@ -486,7 +486,7 @@ int4_stream_v2(V2Args args) {
   const int nchunks = G / kChunkGroups;
   const int items = count_active_experts(p.offsets, args.num_experts) * nb;
   const int st_r = tid >> 3, st_g = tid & 7;
-  const uint32_t kNibMask = 0x000F000Fu;
+  const uint32_t kNibMask = in_vgpr(0x000F000Fu);
   const bf16x8 neg136 = __builtin_bit_cast(bf16x8, u32x4{0xC308C308u, 0xC308C308u, 0xC308C308u, 0xC308C308u});
 
   for (int item = blockIdx.x; item < items; item += gridDim.x) {

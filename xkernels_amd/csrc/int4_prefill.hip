@@ -42,14 +42,22 @@ namespace {
 constexpr int kPBM = 128;              // routed rows per tile
 constexpr int kPBN = 256;              // output columns per tile
 constexpr int kPBK = 128;              // k per pipeline step (4 quantisation groups)
+#ifndef XK_PREFILL_WN
+#define XK_PREFILL_WN 8
+#endif
 constexpr int kWM = 1;                 // waves along the rows
-constexpr int kWN = 8;                 // waves along the columns
+constexpr int kWN = XK_PREFILL_WN;     // waves along the columns
 constexpr int kPWaves = kWM * kWN;
 constexpr int kPThreads = kPWaves * 64;
+constexpr int kStRows = kPThreads / 16;    // activation rows staged per pass
+constexpr int kStPasses = kPBM / kStRows;  // staging passes per step
 constexpr int kRT = kPBM / kWM / 16;   // 16-row MFMA tiles per wave
 constexpr int kCT = kPBN / kWN / 16;   // 16-column MFMA tiles per wave
 constexpr int kPStride = kPBK + 16;    // bf16 per LDS row (72 dwords)
 constexpr int kPMaxExperts = 1024;
+#ifndef XK_PREFILL_INTERLEAVE
+#define XK_PREFILL_INTERLEAVE 0
+#endif
 constexpr int kXcds = 8;               // MI355X: 8 XCDs, workgroups round-robin over them
 
 struct PrefillArgs {
@@ -76,7 +84,7 @@ int4_prefill_gemm(PrefillArgs p) {
   const int steps = K / kPBK;
   const int NB = N / kPBN;
   const int E = p.num_experts;
-  const uint32_t kNibMask = 0x000F000Fu;
+  const uint32_t kNibMask = in_vgpr(0x000F000Fu);
 
   // Row blocks per expert, as an inclusive prefix (wave 0, 64 experts a round).
   if (wave == 0) {
@@ -101,7 +109,7 @@ int4_prefill_gemm(PrefillArgs p) {
   const int t_beg = static_cast<int>(static_cast<int64_t>(T) * xcd / kXcds);
   const int t_end = static_cast<int>(static_cast<int64_t>(T) * (xcd + 1) / kXcds);
 
-  // A staging: thread -> (row st_row + 32 i, 16-byte chunk st_kv). The two
+  // A staging: thread -> (row st_row + kStRows i, 16-byte chunk st_kv). The two
   // 16-lane halves of each 32-lane LDS write group take rows 8 apart, whose
   // bank groups are disjoint.
   const int st_kv = tid & 15, st_g = tid >> 4;
@@ -133,10 +141,10 @@ int4_prefill_gemm(PrefillArgs p) {
 
     // Rows without a token read token 0: MFMA rows are independent and those
     // rows are never stored, so every load stays unconditional.
-    const u32x4* a_src[4];
+    const u32x4* a_src[kStPasses];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int tok = max(tok_lds[st_row + 32 * i], 0);
+    for (int i = 0; i < kStPasses; ++i) {
+      const int tok = max(tok_lds[st_row + kStRows * i], 0);
       a_src[i] = reinterpret_cast<const u32x4*>(p.A + static_cast<int64_t>(tok) * K) + st_kv;
     }
     const u32x4* wrow[kCT];
@@ -148,20 +156,20 @@ int4_prefill_gemm(PrefillArgs p) {
       srow[c] = p.scale + n * G + q;
     }
 
-    auto load_a = [&](int s, u32x4 (&ar)[4]) {
+    auto load_a = [&](int s, u32x4 (&ar)[kStPasses]) {
       s = min(s, steps - 1);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) ar[i] = a_src[i][s * (kPBK / 8)];
+      for (int i = 0; i < kStPasses; ++i) ar[i] = a_src[i][s * (kPBK / 8)];
     };
-    auto store_a = [&](int buf, const u32x4 (&ar)[4]) {
+    auto store_a = [&](int buf, const u32x4 (&ar)[kStPasses]) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
+      for (int i = 0; i < kStPasses; ++i) {
         const uint32_t in[4] = {ar[i][0], ar[i][1], ar[i][2], ar[i][3]};
         uint32_t o[4];
         perm8(in, o);
         // global chunk st_kv = 4 q + j goes to chunk 4 j + q
         *reinterpret_cast<u32x4*>(
-            &a_lds[buf][(st_row + 32 * i) * kPStride + ((st_kv & 3) * 4 + (st_kv >> 2)) * 8]) =
+            &a_lds[buf][(st_row + kStRows * i) * kPStride + ((st_kv & 3) * 4 + (st_kv >> 2)) * 8]) =
             u32x4{o[0], o[1], o[2], o[3]};
       }
     };
@@ -202,33 +210,54 @@ int4_prefill_gemm(PrefillArgs p) {
             acc[i][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], b, acc[i][c], 0, 0, 0);
         }
       }
+#if XK_PREFILL_INTERLEAVE
+      // interleave: each MFMA followed by a few VALU (dequant of later words)
+      // and, every other MFMA, one LDS read
+#pragma unroll
+      for (int m = 0; m < 4 * kRT * kCT / 2; ++m) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
+      }
+#endif
     };
 
-    u32x4 ar[4], w0[kCT], w1[kCT];
+    u32x4 a0[kStPasses], a1[kStPasses], w0[kCT], w1[kCT];
     uint32_t s0[kCT], s1[kCT];
+    // Prologue: A(0) staged, then the loads in the order the loop leaves them
+    // outstanding at its head (A(s+1), W(s), A(s+2), W(s+1)), so the load
+    // counter waits the compiler derives for both paths into the loop agree.
+    load_a(0, a0);
+    store_a(0, a0);
+    load_a(1, a1);
+    __builtin_amdgcn_sched_barrier(0);
     load_w(0, w0, s0);
+    __builtin_amdgcn_sched_barrier(0);
+    load_a(2, a0);
+    __builtin_amdgcn_sched_barrier(0);
     load_w(1, w1, s1);
-    load_a(0, ar);
-    store_a(0, ar);
-    load_a(1, ar);
-    // step s: A(s+1) -> LDS buffer (s+1)&1 (freed by compute(s-1)); request
-    // A(s+2); contract step s; refill the consumed weight registers with
-    // W(s+2), so a weight load is two steps old when it is used.
+    __builtin_amdgcn_sched_barrier(0);
+    // step s: A(s+1) -> LDS buffer (s+1)&1 (freed by compute(s-1)) from the
+    // register set that then takes A(s+3); contract step s; refill the
+    // consumed weight registers with W(s+2). Activation and weight loads are
+    // thus two steps old when they are used.
     // (scheduling barriers keep the compiler from sinking the activation loads
     // to their use or hoisting the next store's permutes into compute(), either
     // of which would make a step wait for loads issued in the same step)
-    auto step = [&](int s, u32x4 (&w)[kCT], uint32_t (&sv)[kCT]) {
+    auto step = [&](int s, u32x4 (&ar)[kStPasses], u32x4 (&w)[kCT], uint32_t (&sv)[kCT]) {
       __syncthreads();
       store_a((s + 1) & 1, ar);
-      load_a(s + 2, ar);
+      load_a(s + 3, ar);
       __builtin_amdgcn_sched_barrier(0);
       compute(s & 1, w, sv);
       __builtin_amdgcn_sched_barrier(0);
       load_w(s + 2, w, sv);
     };
     for (int s = 0; s < steps; s += 2) {
-      step(s, w0, s0);
-      step(s + 1, w1, s1);
+      step(s, a1, w0, s0);
+      step(s + 1, a0, w1, s1);
     }
 
 #pragma unroll
