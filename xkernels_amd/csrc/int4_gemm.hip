@@ -649,10 +649,19 @@ int4_stream_v2(V2Args args) {
       for (int pc = 0; pc < kSuper; ++pc) store_spiece(0, pc, load_spiece(0, pc));
       load_a(0, areg);
       store_a(0, areg);
-      load_a(1, areg);
+      // Issue the rest in the order the loop leaves its loads outstanding at
+      // its head (W(c+1), A(c+1), W(c+2)): the load-counter wait the compiler
+      // derives at the loop head covers both paths into it, and a prologue
+      // that ends with the activation loads would make it a full drain.
+      __builtin_amdgcn_sched_barrier(0);
       load_w(0, w0);
+      __builtin_amdgcn_sched_barrier(0);
       load_w(1, w1);
+      __builtin_amdgcn_sched_barrier(0);
+      load_a(1, areg);
+      __builtin_amdgcn_sched_barrier(0);
       load_w(2, w2);
+      __builtin_amdgcn_sched_barrier(0);
       uint2 spiece = make_uint2(0u, 0u);
       // step c: A(c+1) -> LDS buffer (c+1)&1 (freed by compute(c-1)); the scale
       // piece loaded at step c-1 -> LDS; request A(c+2), scale piece (c/8+1, c%8)
