@@ -33,8 +33,13 @@
 // dequant rounded to A's dtype like the reference. Correctness fallback for the
 // fp32 sweep points and unusual group sizes.
 #include <algorithm>
+#include <type_traits>
 
 #include "int4_common.h"
+
+#ifndef XK_INT4_STREAM_WAVES
+#define XK_INT4_STREAM_WAVES 4
+#endif
 
 namespace xk {
 namespace {
@@ -466,15 +471,17 @@ __device__ __forceinline__ int count_active_experts(const int32_t* offsets, int 
   return n;
 }
 
-template <Int4Mode MODE>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+template <Int4Mode MODE, int WAVES>
+__global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 int4_stream_v2(V2Args args) {
   constexpr bool kFast = MODE == Int4Mode::kFast;
+  constexpr int kThreads = WAVES * 64;
+  constexpr int kCols = WAVES * kColsPerWave;  // output columns per work item
   constexpr int kWRing = 4;       // weight chunks in registers (prefetch distance 3)
   constexpr int kSuper = 8;       // chunks per scale superchunk: 64 groups = 128 B per row
   constexpr int kSStride = 72;    // bf16 per scale row in LDS (128 B + 16 B pad)
   __shared__ __attribute__((aligned(16))) uint16_t a_lds[2][kV2Rows * kV2Stride];
-  __shared__ __attribute__((aligned(16))) uint16_t s_lds[kWaves][2][32 * kSStride];
+  __shared__ __attribute__((aligned(16))) uint16_t s_lds[WAVES][2][32 * kSStride];
   __shared__ int slot_lds[kV2Rows];
   __shared__ int tok_lds[kV2Rows];
   const StreamArgs& p = args.s;
@@ -482,16 +489,15 @@ int4_stream_v2(V2Args args) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int c16 = lane & 15, q = lane >> 4;
   const int K = p.K, N = p.N, G = K >> 5, KW = K >> 3;
-  const int nb = (N + kColsPerWG - 1) / kColsPerWG;
+  const int nb = (N + kCols - 1) / kCols;
   const int nchunks = G / kChunkGroups;
   const int items = count_active_experts(p.offsets, args.num_experts) * nb;
-  const int st_r = tid >> 3, st_g = tid & 7;
   const uint32_t kNibMask = in_vgpr(0x000F000Fu);
   const bf16x8 neg136 = __builtin_bit_cast(bf16x8, u32x4{0xC308C308u, 0xC308C308u, 0xC308C308u, 0xC308C308u});
 
   for (int item = blockIdx.x; item < items; item += gridDim.x) {
     const int e = find_active_expert(p.offsets, args.num_experts, item / nb);
-    const int n_base = (item % nb) * kColsPerWG + wave * kColsPerWave;
+    const int n_base = (item % nb) * kCols + wave * kColsPerWave;
     const int beg = p.offsets[e], end = p.offsets[e + 1];
     const uint32_t* wrow[2];
 #pragma unroll
@@ -517,18 +523,28 @@ int4_stream_v2(V2Args args) {
         tok_lds[tid] = tok;
       }
       __syncthreads();
+      // The pass body is compiled for one and for two 16-row tiles, so that
+      // only the rows in use are staged and every count below is a constant.
+      auto body = [&](auto nt_tag) {
+      constexpr int NT = decltype(nt_tag)::value;
+      // Activation staging: NT*16 rows x 32 16-byte vectors per chunk; thread
+      // -> row st_r, vectors v0 .. v0 + kVec - 1 (vector v = 4 g + j: group g,
+      // subgroup j).
+      constexpr int kVec = NT * 16 * 32 / kThreads;
+      constexpr int kTPR = 32 / kVec;  // threads per row
+      const int st_r = tid / kTPR, v0 = (tid % kTPR) * kVec;
       // Rows without a token read row 0: MFMA rows are independent and those
       // rows are never stored, so no branch (and no load-counter drain).
       const int my_tok = max(tok_lds[st_r], 0);
       const u32x4* a_src =
-          reinterpret_cast<const u32x4*>(p.A + static_cast<int64_t>(my_tok) * K) + st_g * 4;
+          reinterpret_cast<const u32x4*>(p.A + static_cast<int64_t>(my_tok) * K) + v0;
 
       // Every global load below is unconditional (indices clamped) so the
       // compiler keeps counting outstanding loads across the ring.
       auto load_a = [&](int chunk, u32x4* ar) {
         chunk = min(chunk, nchunks - 1);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) ar[j] = a_src[chunk * (kChunkK / 8) + j];
+        for (int i = 0; i < kVec; ++i) ar[i] = a_src[chunk * (kChunkK / 8) + i];
       };
       auto store_a = [&](int buf, const u32x4* ar) {
         // Both dequant forms emit the pair order (d, d + 4); stage A to match.
@@ -539,10 +555,11 @@ int4_stream_v2(V2Args args) {
         // and the 16 rows are 136 dwords apart: bank-conflict free.
         uint32_t* row = reinterpret_cast<uint32_t*>(&a_lds[buf][st_r * kV2Stride]);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          uint32_t in[4] = {ar[j][0], ar[j][1], ar[j][2], ar[j][3]}, o[4];
+        for (int i = 0; i < kVec; ++i) {
+          uint32_t in[4] = {ar[i][0], ar[i][1], ar[i][2], ar[i][3]}, o[4];
           perm8(in, o);
-          const int off = (st_g >> 2) * 64 + (kFast ? (st_g & 3) * 16 + j * 4 : j * 16 + (st_g & 3) * 4);
+          const int g = (v0 + i) >> 2, j = (v0 + i) & 3;
+          const int off = (g >> 2) * 64 + (kFast ? (g & 3) * 16 + j * 4 : j * 16 + (g & 3) * 4);
           *reinterpret_cast<u32x4*>(row + off) = u32x4{o[0], o[1], o[2], o[3]};
         }
       };
@@ -600,7 +617,7 @@ int4_stream_v2(V2Args args) {
               }
 #pragma unroll
               for (int t = 0; t < 2; ++t) {
-                if (t >= ntiles) break;
+                if (t >= NT) break;
                 const bf16x8 afrag = *reinterpret_cast<const bf16x8*>(
                     &a_lds[buf][(t * 16 + c16) * kV2Stride + 2 * (h * 64 + j * 16 + q * 4)]);
                 const f32x4 d2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
@@ -629,7 +646,7 @@ int4_stream_v2(V2Args args) {
               for (int c = 0; c < 2; ++c) bfrag[c] = dequant_rne(wr[c][h][j], s[c], ms[c], kNibMask);
 #pragma unroll
               for (int t = 0; t < 2; ++t) {
-                if (t >= ntiles) break;
+                if (t >= NT) break;
                 const bf16x8 afrag = *reinterpret_cast<const bf16x8*>(
                     &a_lds[buf][(t * 16 + c16) * kV2Stride + 2 * (h * 64 + j * 16 + q * 4)]);
 #pragma unroll
@@ -643,7 +660,7 @@ int4_stream_v2(V2Args args) {
 
       // Prologue: scale superchunk 0 and activation chunk 0 in LDS, A(1) and
       // W(0..2) in flight.
-      u32x4 areg[4];
+      u32x4 areg[kVec];
       u32x4 w0[2][2], w1[2][2], w2[2][2], w3[2][2];
 #pragma unroll
       for (int pc = 0; pc < kSuper; ++pc) store_spiece(0, pc, load_spiece(0, pc));
@@ -686,7 +703,7 @@ int4_stream_v2(V2Args args) {
 
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
-        if (t >= ntiles) break;
+        if (t >= NT) break;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int slot = slot_lds[t * 16 + q * 4 + i];
@@ -698,6 +715,11 @@ int4_stream_v2(V2Args args) {
           }
         }
       }
+      };
+      if (ntiles == 2)
+        body(std::integral_constant<int, 2>{});
+      else
+        body(std::integral_constant<int, 1>{});
     }
   }
 }
@@ -805,12 +827,14 @@ int launch_int4_gemm(const void* A, int a_dtype, int64_t M, int64_t K, const int
                  int((K / 32) % 8 == 0 && reinterpret_cast<uintptr_t>(scale) % 16 == 0)};
     if (K % 256 == 0 && a.scale_vec && !(flags & XK_INT4_V1)) {
       V2Args v2{a, int(E)};
-      const int64_t items = E * cdiv(N, kColsPerWG);
-      const dim3 g2(static_cast<unsigned>(std::min<int64_t>(items, 2 * device_cu_count())));
+      constexpr int kW = XK_INT4_STREAM_WAVES;
+      constexpr int kPerCu = kW == 8 ? 1 : 2;  // LDS of the scale superchunks limits residency
+      const int64_t items = E * cdiv(N, kW * kColsPerWave);
+      const dim3 g2(static_cast<unsigned>(std::min<int64_t>(items, kPerCu * device_cu_count())));
       if (flags & XK_INT4_FAST_DEQUANT)
-        hipLaunchKernelGGL((int4_stream_v2<Int4Mode::kFast>), g2, dim3(256), 0, stream, v2);
+        hipLaunchKernelGGL((int4_stream_v2<Int4Mode::kFast, kW>), g2, dim3(kW * 64), 0, stream, v2);
       else
-        hipLaunchKernelGGL((int4_stream_v2<Int4Mode::kRne>), g2, dim3(256), 0, stream, v2);
+        hipLaunchKernelGGL((int4_stream_v2<Int4Mode::kRne, kW>), g2, dim3(kW * 64), 0, stream, v2);
       XK_CHECK_LAUNCH("int4_stream_v2");
       return XK_OK;
     }
