@@ -492,7 +492,7 @@ int4_stream_v2(V2Args args) {
   const int nb = (N + kCols - 1) / kCols;
   const int nchunks = G / kChunkGroups;
   const int items = count_active_experts(p.offsets, args.num_experts) * nb;
-  const uint32_t kNibMask = in_vgpr(0x000F000Fu);
+  const uint32_t kNibMask = in_vgpr(0x000F000Fu), kNibMaskHi = in_vgpr(0x00F000F0u);
   const bf16x8 neg136 = __builtin_bit_cast(bf16x8, u32x4{0xC308C308u, 0xC308C308u, 0xC308C308u, 0xC308C308u});
 
   for (int item = blockIdx.x; item < items; item += gridDim.x) {
@@ -631,19 +631,18 @@ int4_stream_v2(V2Args args) {
               }
             }
           } else {
-            float s[2], ms[2];
+            RneScale ks[2];
 #pragma unroll
             for (int c = 0; c < 2; ++c) {
               // scale of group 4h + q: word 2h + (q >> 1), half q & 1
               const uint32_t lo = (q & 2) ? sr[c][2 * h + 1] : sr[c][2 * h];
-              s[c] = __uint_as_float((q & 1) ? (lo & 0xFFFF0000u) : (lo << 16));
-              ms[c] = -1032.0f * s[c];
+              ks[c] = rne_scale(__uint_as_float((q & 1) ? (lo & 0xFFFF0000u) : (lo << 16)));
             }
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
               bf16x8 bfrag[2];
 #pragma unroll
-              for (int c = 0; c < 2; ++c) bfrag[c] = dequant_rne(wr[c][h][j], s[c], ms[c], kNibMask);
+              for (int c = 0; c < 2; ++c) bfrag[c] = dequant_rne(wr[c][h][j], ks[c], kNibMask, kNibMaskHi);
 #pragma unroll
               for (int t = 0; t < 2; ++t) {
                 if (t >= NT) break;

@@ -84,7 +84,7 @@ int4_prefill_gemm(PrefillArgs p) {
   const int steps = K / kPBK;
   const int NB = N / kPBN;
   const int E = p.num_experts;
-  const uint32_t kNibMask = in_vgpr(0x000F000Fu);
+  const uint32_t kNibMask = in_vgpr(0x000F000Fu), kNibMaskHi = in_vgpr(0x00F000F0u);
 
   // Row blocks per expert, as an inclusive prefix (wave 0, 64 experts a round).
   if (wave == 0) {
@@ -189,12 +189,9 @@ int4_prefill_gemm(PrefillArgs p) {
       for (int c = 0; c < kCT; ++c) acc[i][c] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     auto compute = [&](int buf, const u32x4 (&w)[kCT], const uint32_t (&sv)[kCT]) {
-      float s[kCT], ms[kCT];
+      RneScale ks[kCT];
 #pragma unroll
-      for (int c = 0; c < kCT; ++c) {
-        s[c] = __uint_as_float(sv[c] << 16);
-        ms[c] = -1032.0f * s[c];
-      }
+      for (int c = 0; c < kCT; ++c) ks[c] = rne_scale(__uint_as_float(sv[c] << 16));
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         bf16x8 af[kRT];
@@ -204,7 +201,7 @@ int4_prefill_gemm(PrefillArgs p) {
               &a_lds[buf][(wm * kRT * 16 + i * 16 + c16) * kPStride + (j * 4 + q) * 8]);
 #pragma unroll
         for (int c = 0; c < kCT; ++c) {
-          const bf16x8 b = dequant_rne(w[c][j], s[c], ms[c], kNibMask);
+          const bf16x8 b = dequant_rne(w[c][j], ks[c], kNibMask, kNibMaskHi);
 #pragma unroll
           for (int i = 0; i < kRT; ++i)
             acc[i][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], b, acc[i][c], 0, 0, 0);
