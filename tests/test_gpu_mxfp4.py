@@ -64,11 +64,15 @@ def test_fp32_activations(dev):
     assert_close(got, _ref(A, wts, ids, w), 2e-2, 2e-2, "fp32 A")
 
 
-def test_full_scale_range_and_special_codes(dev):
-    """Scale bytes across [1, 254] plus 0xFF (reads as 0)."""
-    A, wts, ids, w = _case(6, 4, 256, 64, 2, seed=6, scale_lo=110, scale_hi=135)
+@pytest.mark.parametrize("ispp", [64, 256])
+def test_full_scale_range_and_special_codes(ispp, dev):
+    """Scale bytes across [110, 135) plus 0xFF (reads as 0) and 0 (2^-127) in both
+    the 256-k stream kernel and the generic kernel (ispp 64)."""
+    A, wts, ids, w = _case(6, 4, 256, ispp, 2, seed=6, scale_lo=110, scale_hi=135)
     wts["w2_scale"][0, :3, 0] = 255
     wts["w13_scale"][1, 5, 2] = 255
+    wts["w13_scale"][2, 7, 1] = 0
+    wts["w2_scale"][3, 9, 1] = 0
     got = _run(A, wts, ids, w, dev)
     assert_close(got, _ref(A, wts, ids, w), 2e-2, 2e-2, "scale range")
 

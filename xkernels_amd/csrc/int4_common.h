@@ -1,4 +1,5 @@
-// Device helpers shared by the INT4 GEMM kernels (decode stream and prefill tile).
+// Device helpers shared by the 4-bit weight GEMM kernels (INT4 decode stream and
+// prefill tile, MXFP4 stream).
 #pragma once
 
 #include "common.h"
@@ -83,6 +84,37 @@ __device__ __forceinline__ bf16x8 dequant_magic(uint32_t w, uint32_t mask) {
 #pragma unroll
   for (int d = 0; d < 4; ++d) b[d] = and_or(w >> (4 * d), mask, 0x43004300u);
   return __builtin_bit_cast(bf16x8, b);
+}
+
+// Persistent kernels enumerate work over the experts that received slots:
+// the padded align offsets give each expert's range; empty experts are skipped.
+__device__ __forceinline__ int find_active_expert(const int32_t* offsets, int E, int rank) {
+  // index of the rank-th expert with a non-empty padded range (all lanes agree)
+  const int lane = threadIdx.x & 63;
+  int seen = 0;
+  for (int base = 0; base < E; base += 64) {
+    const int e = base + lane;
+    const bool act = e < E && offsets[e + 1] > offsets[e];
+    const uint64_t m = __ballot(act);
+    const int cnt = __popcll(m);
+    if (rank < seen + cnt) {
+      uint64_t mm = m;
+      for (int r = rank - seen; r > 0; --r) mm &= mm - 1;  // drop lower set bits
+      return base + __ffsll(static_cast<long long>(mm)) - 1;
+    }
+    seen += cnt;
+  }
+  return -1;
+}
+
+__device__ __forceinline__ int count_active_experts(const int32_t* offsets, int E) {
+  const int lane = threadIdx.x & 63;
+  int n = 0;
+  for (int base = 0; base < E; base += 64) {
+    const int e = base + lane;
+    n += __popcll(__ballot(e < E && offsets[e + 1] > offsets[e]));
+  }
+  return n;
 }
 
 }  // namespace xk

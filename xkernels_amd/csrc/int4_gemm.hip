@@ -442,35 +442,6 @@ struct V2Args {
   int num_experts;
 };
 
-__device__ __forceinline__ int find_active_expert(const int32_t* offsets, int E, int rank) {
-  // index of the rank-th expert with a non-empty padded range (all lanes agree)
-  const int lane = threadIdx.x & 63;
-  int seen = 0;
-  for (int base = 0; base < E; base += 64) {
-    const int e = base + lane;
-    const bool act = e < E && offsets[e + 1] > offsets[e];
-    const uint64_t m = __ballot(act);
-    const int cnt = __popcll(m);
-    if (rank < seen + cnt) {
-      uint64_t mm = m;
-      for (int r = rank - seen; r > 0; --r) mm &= mm - 1;  // drop lower set bits
-      return base + __ffsll(static_cast<long long>(mm)) - 1;
-    }
-    seen += cnt;
-  }
-  return -1;
-}
-
-__device__ __forceinline__ int count_active_experts(const int32_t* offsets, int E) {
-  const int lane = threadIdx.x & 63;
-  int n = 0;
-  for (int base = 0; base < E; base += 64) {
-    const int e = base + lane;
-    n += __popcll(__ballot(e < E && offsets[e + 1] > offsets[e]));
-  }
-  return n;
-}
-
 template <Int4Mode MODE, int WAVES>
 __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 int4_stream_v2(V2Args args) {
