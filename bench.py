@@ -185,7 +185,12 @@ def secondary(a) -> dict:
     if a.workload == "c3-align":
         M, k, E, bs = 16384, 8, 48, 16
         ids = _zipf_topk(M, k, E, 1.1, a.seed).cuda()
-        ms = _event_time(lambda: moe_align_block_size(ids, bs, E, backend=hip), a.steps, a.warmup)
+        from xkernels_amd import MoeAlignWorkspace
+
+        ws = MoeAlignWorkspace.allocate(M, k, E, bs, device="cuda")
+        # truncate=False: the sync-free form (truncate=True reads num_post back to the host)
+        ms = _event_time(lambda: moe_align_block_size(ids, bs, E, backend=hip, truncate=False, workspace=ws),
+                         a.steps, a.warmup)
         numel = M * k
         max_pad = numel + (E + 1) * (bs - 1)
         nbytes = numel * 4 + max_pad * 4 + (max_pad // bs) * 4  # ids in, sorted + expert ids out

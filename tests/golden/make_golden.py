@@ -31,21 +31,26 @@ def _bf16_bits(t: torch.Tensor) -> np.ndarray:
 
 def align_cases() -> dict[str, np.ndarray]:
     out = {}
+    # the last three exceed one workgroup (numel > 8192): the grid path
     cases = [("tiny", 3, 2, 3, 2, 0), ("decode", 64, 8, 48, 16, 1), ("skew", 40, 6, 8, 16, 2),
-             ("bs1", 9, 3, 5, 1, 3), ("ep", 32, 4, 16, 8, 4)]
+             ("bs1", 9, 3, 5, 1, 3), ("ep", 32, 4, 16, 8, 4), ("grid", 1500, 8, 48, 16, 5),
+             ("grid_wide", 1100, 8, 600, 4, 6), ("grid_ep", 1300, 8, 64, 64, 7)]
     for name, M, k, E, bs, seed in cases:
         g = torch.Generator().manual_seed(seed)
         if name == "skew":  # every slot on experts 0/1: most blocks pad-only tails
             ids = torch.randint(0, 2, (M, k), generator=g, dtype=torch.int32)
+        elif name.startswith("grid"):  # Zipf-like expert popularity
+            p = 1.0 / torch.arange(1, E + 1, dtype=torch.float64) ** 1.1
+            ids = torch.multinomial(p.expand(M, E), k, replacement=False, generator=g).to(torch.int32)
         else:
             ids = torch.randint(0, E, (M, k), generator=g, dtype=torch.int32)
         emap = None
         nl = E
-        if name == "ep":
+        if name in ("ep", "grid_ep"):
+            nl = 8 if name == "ep" else 24
             emap = torch.full((E,), -1, dtype=torch.int32)
-            emap[4:12] = torch.arange(8, dtype=torch.int32)
+            emap[4:4 + nl] = torch.arange(nl, dtype=torch.int32)
             s, e, n = R.moe_align_block_size_ep(ids, bs, E, emap)
-            nl = 8
         else:
             s, e, n = R.moe_align_block_size_ref(ids, bs, E, truncate=False)
         out[f"align_{name}_ids"] = ids.numpy()

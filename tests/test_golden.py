@@ -16,7 +16,7 @@ from oracle import c_oracle
 from oracle import torch_ref as R
 
 G = np.load(Path(__file__).resolve().parent / "golden" / "moe_golden.npz")
-ALIGN = ["tiny", "decode", "skew", "bs1", "ep"]
+ALIGN = ["tiny", "decode", "skew", "bs1", "ep", "grid", "grid_wide", "grid_ep"]
 
 
 def _t(key):
@@ -33,8 +33,8 @@ def _bf16(key):
 def test_oracles_reproduce_align_fixture(name):
     ids = _t(f"align_{name}_ids")
     bs, nl = (int(x) for x in G[f"align_{name}_meta"])
-    if name == "ep":
-        emap = _t("align_ep_emap")
+    if name in ("ep", "grid_ep"):
+        emap = _t(f"align_{name}_emap")
         s, e, n = R.moe_align_block_size_ep(ids, bs, emap.numel(), emap)
         cs, ce, cn = c_oracle.align(ids, bs, nl, expert_map=emap)
         assert torch.equal(cs, s)
@@ -87,9 +87,9 @@ def test_hip_align_matches_fixture(name, dev):
     sorted_ids = torch.full((max_pad,), -7, dtype=torch.int32, device=dev)
     expert_ids = torch.full(((max_pad + bs - 1) // bs,), -7, dtype=torch.int32, device=dev)
     num_post = torch.empty(1, dtype=torch.int32, device=dev)
-    ws = torch.empty(max(1, _lib.query("xk_moe_align_workspace_bytes", numel, nl)), dtype=torch.uint8,
-                     device=dev)
-    emap = _t("align_ep_emap").to(dev) if name == "ep" else None
+    ws = torch.full((max(1, _lib.query("xk_moe_align_workspace_bytes", numel, nl)),), 0x7F,
+                    dtype=torch.uint8, device=dev)  # stale scratch must not matter
+    emap = _t(f"align_{name}_emap").to(dev) if name in ("ep", "grid_ep") else None
     stream = torch.cuda.current_stream().cuda_stream
     _lib.call("xk_moe_align_block_size", ids.data_ptr(), numel, nl, bs,
               None if emap is None else emap.data_ptr(), 0 if emap is None else emap.numel(),

@@ -6,17 +6,18 @@
 // run is padded to a block_size multiple with pad id = numel, one expert id is
 // emitted per block and unused trailing blocks read 0 (w4a16.py:91-96).
 //
-// Design (MI355X): counting sort in three phases that share device functions.
+// Design (MI355X): counting sort from three steps that share device functions.
 //   count   : LDS histogram of a contiguous slot chunk per workgroup (LDS atomics)
-//   scan    : per-expert exclusive prefix over the chunk histograms, padded
-//             prefix over experts (wavefront shuffle scan), expert_ids by
+//   layout  : padded prefix over experts (wavefront shuffle scan), expert_ids by
 //             binary search of the padded prefix, pad ids only into the gaps
 //   scatter : stable in-chunk ranks from wavefront ballots. Lanes holding the
 //             same expert find each other with one ballot per key bit; rank =
 //             popcount(peers below me); waves are ordered through a small
 //             per-wave LDS count table.
-// Small problems run all three phases in ONE workgroup (one launch); large ones
-// use a grid for count and scatter with a one-workgroup scan in between.
+// Small problems run all three in ONE workgroup (one launch). Large ones launch
+// a histogram grid, then one grid in which every workgroup re-derives the
+// expert layout from the chunk histograms, scatters its chunk and writes its
+// slice of expert_ids and pad ids (two launches, no single-workgroup phase).
 #include <algorithm>
 
 #include "common.h"
@@ -205,82 +206,105 @@ align_count(const int32_t* __restrict__ ids, int64_t numel, int64_t chunk,
     chunk_cnt[static_cast<int64_t>(blockIdx.x) * num_experts + i] = lds[i];
 }
 
-// Grid phase 2 (one workgroup of 1024): chunk_cnt[b][e] becomes the exclusive
-// prefix over chunks b; experts are laid out and everything but the real slots
-// is written. Thread (e, part) owns a contiguous range of chunks of expert e so
-// the column prefix is two short passes of independent loads.
+// Grid phase 2: every workgroup b of 1024 threads
+//   * sums the chunk histograms column-wise: total count of every expert and
+//     the count in chunks before b (independent loads, threads (expert, part));
+//   * forms the padded expert prefix (block scan);
+//   * stably scatters its own chunk;
+//   * writes its 1/nchunks slice of expert_ids and of the pad ids (gap slots of
+//     every expert and the tail), so the layout is written by the whole grid.
+// Workgroup 0 also writes num_tokens_post_padded and expert_offsets.
 __global__ void __launch_bounds__(1024)
-align_scan(int32_t* __restrict__ chunk_cnt, int nchunks, int num_experts,
-           int block_size, int64_t numel, int64_t max_pad, int64_t max_blocks,
-           int32_t* __restrict__ sorted_ids, int32_t* __restrict__ expert_ids,
-           int32_t* __restrict__ num_post, int32_t* __restrict__ expert_offsets,
-           int32_t* __restrict__ off_out) {
-  extern __shared__ int lds[];
-  int* cnt = lds;                        // [E]
-  int* off = cnt + num_experts;          // [E+1]
-  int* wsum = off + num_experts + 1;     // [16]
-  int* part = wsum + 16;                 // [parts][E] <= 1024
-  const int parts = max(1, static_cast<int>(blockDim.x) / num_experts);
-  const int e = threadIdx.x % num_experts, p = threadIdx.x / num_experts;
-  const int per = static_cast<int>(cdiv(nchunks, parts));
-  const int b0 = p * per, b1 = min(nchunks, b0 + per);
-  if (p < parts) {
-    int s = 0;
-#pragma unroll 8
-    for (int b = b0; b < b1; ++b) s += chunk_cnt[static_cast<int64_t>(b) * num_experts + e];
-    part[p * num_experts + e] = s;
-  }
-  __syncthreads();
-  if (threadIdx.x < num_experts) {
-    int run = 0;
-    for (int q = 0; q < parts; ++q) {
-      int v = part[q * num_experts + threadIdx.x];
-      part[q * num_experts + threadIdx.x] = run;
-      run += v;
-    }
-    cnt[threadIdx.x] = run;
-  }
-  __syncthreads();
-  if (p < parts) {
-    int run = part[p * num_experts + e];
-    for (int b = b0; b < b1; b += 8) {
-      int v[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i)
-        v[i] = (b + i < b1) ? chunk_cnt[static_cast<int64_t>(b + i) * num_experts + e] : 0;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        if (b + i < b1) chunk_cnt[static_cast<int64_t>(b + i) * num_experts + e] = run;
-        run += v[i];
-      }
-    }
-  }
-  __syncthreads();
-  emit_layout(cnt, off, wsum, num_experts, block_size, numel, max_pad, max_blocks,
-              sorted_ids, expert_ids, num_post, expert_offsets);
-  __syncthreads();
-  for (int i = threadIdx.x; i <= num_experts; i += blockDim.x) off_out[i] = off[i];
-}
-
-// Grid phase 3: stable scatter of chunk b.
-__global__ void __launch_bounds__(256)
-align_scatter(const int32_t* __restrict__ ids, int64_t numel, int64_t chunk,
-              int num_experts, const int32_t* __restrict__ emap, int num_global,
-              const int32_t* __restrict__ chunk_cnt, const int32_t* __restrict__ off,
-              int32_t* __restrict__ sorted_ids) {
+align_place(const int32_t* __restrict__ ids, int64_t numel, int64_t chunk, int nchunks,
+            int num_experts, int block_size, const int32_t* __restrict__ emap,
+            int num_global, const int32_t* __restrict__ chunk_cnt, int64_t max_pad,
+            int64_t max_blocks, int32_t* __restrict__ sorted_ids,
+            int32_t* __restrict__ expert_ids, int32_t* __restrict__ num_post,
+            int32_t* __restrict__ expert_offsets) {
   extern __shared__ int lds[];
   const int nw = blockDim.x >> 6;
-  int* base = lds;                      // [E]
-  int* tot = base + num_experts;        // [E]
-  int* wavecnt = tot + num_experts;     // [nw][E+1]
-  for (int e = threadIdx.x; e < num_experts; e += blockDim.x)
-    base[e] = off[e] + chunk_cnt[static_cast<int64_t>(blockIdx.x) * num_experts + e];
-  for (int i = threadIdx.x; i < nw * (num_experts + 1); i += blockDim.x) wavecnt[i] = 0;
+  int* tot = lds;                          // [E]   total count of expert e
+  int* base = tot + num_experts;           // [E]   count before this chunk, then cursor
+  int* off = base + num_experts;           // [E+1] padded prefix
+  int* wsum = off + num_experts + 1;       // [16]
+  int* ctot = wsum + 16;                   // [E]   scatter scratch
+  int* wavecnt = ctot + num_experts;       // [nw][E+1]
+  int* part = wavecnt + nw * (num_experts + 1);  // [parts][2][E]
+  const int b = blockIdx.x, tid = threadIdx.x;
+  const int parts = max(1, static_cast<int>(blockDim.x) / num_experts);
+  for (int i = tid; i < nw * (num_experts + 1); i += blockDim.x) wavecnt[i] = 0;
+  {
+    // thread (e, p): chunks [p*per, (p+1)*per) of expert e (for e < E when
+    // E <= blockDim; otherwise one part and a loop over the experts)
+    const int per = static_cast<int>(cdiv(nchunks, parts));
+    for (int idx = tid; idx < parts * num_experts; idx += blockDim.x) {
+      const int e = idx % num_experts, p = idx / num_experts;
+      const int b0 = p * per, b1 = min(nchunks, b0 + per);
+      int all = 0, before = 0;
+      for (int c = b0; c < b1; ++c) {
+        const int v = chunk_cnt[static_cast<int64_t>(c) * num_experts + e];
+        all += v;
+        before += c < b ? v : 0;
+      }
+      part[(2 * p) * num_experts + e] = all;
+      part[(2 * p + 1) * num_experts + e] = before;
+    }
+  }
   __syncthreads();
-  const int64_t begin = blockIdx.x * chunk;
-  const int64_t end = min(numel, begin + chunk);
-  chunk_stable_scatter(ids, begin, end, emap, num_global, num_experts, base, wavecnt, tot,
-                       sorted_ids);
+  for (int e = tid; e < num_experts; e += blockDim.x) {
+    int all = 0, before = 0;
+    for (int p = 0; p < parts; ++p) {
+      all += part[(2 * p) * num_experts + e];
+      before += part[(2 * p + 1) * num_experts + e];
+    }
+    tot[e] = all;
+    base[e] = before;
+  }
+  __syncthreads();
+  // padded exclusive prefix over experts (num_experts <= blockDim)
+  const int c = tid < num_experts ? tot[tid] : 0;
+  const int padded = ((c + block_size - 1) / block_size) * block_size;
+  int total = 0;
+  const int ex = block_exclusive_scan(padded, wsum, &total);
+  if (tid < num_experts) {
+    off[tid] = ex;
+    base[tid] += ex;
+  }
+  if (tid == 0) off[num_experts] = total;
+  __syncthreads();
+  if (b == 0) {
+    if (tid == 0) num_post[0] = total;
+    if (expert_offsets != nullptr)
+      for (int e = tid; e <= num_experts; e += blockDim.x) expert_offsets[e] = off[e];
+  }
+  // this chunk's slots
+  const int64_t begin = static_cast<int64_t>(b) * chunk;
+  chunk_stable_scatter(ids, begin, min(numel, begin + chunk), emap, num_global, num_experts,
+                       base, wavecnt, ctot, sorted_ids);
+  // slice of the layout: expert of a position = #{e in [1, E] : off[e] <= pos}
+  auto expert_at = [&](int64_t pos) {
+    int lo = 1, hi = num_experts;
+    while (lo <= hi) {
+      const int mid = (lo + hi) >> 1;
+      if (off[mid] <= pos) lo = mid + 1; else hi = mid - 1;
+    }
+    return lo - 1;
+  };
+  const int64_t bper = cdiv(max_blocks, nchunks);
+  for (int64_t i = b * bper + tid; i < min(max_blocks, (b + 1) * bper); i += blockDim.x) {
+    const int64_t pos = i * block_size;
+    expert_ids[i] = pos < total ? expert_at(pos) : 0;
+  }
+  const int32_t pad = static_cast<int32_t>(numel);
+  const int64_t sper = cdiv(max_pad, nchunks);
+  for (int64_t sidx = b * sper + tid; sidx < min(max_pad, (b + 1) * sper); sidx += blockDim.x) {
+    bool gap = sidx >= total;
+    if (!gap) {
+      const int e = expert_at(sidx);
+      gap = sidx - off[e] >= tot[e];
+    }
+    if (gap) sorted_ids[sidx] = pad;
+  }
 }
 
 constexpr int64_t kSingleWgMaxSlots = 8192;
@@ -297,7 +321,7 @@ bool use_single_wg(int64_t numel, int num_experts) {
 int64_t align_workspace_bytes(int64_t numel, int num_experts) {
   if (use_single_wg(numel, num_experts)) return 0;
   const int64_t nchunks = std::max<int64_t>(1, cdiv(numel, kGridChunk));
-  return (nchunks * num_experts + (num_experts + 1)) * static_cast<int64_t>(sizeof(int32_t));
+  return nchunks * num_experts * static_cast<int64_t>(sizeof(int32_t));
 }
 
 int launch_align(const int32_t* ids, int64_t numel, int num_experts, int block_size,
@@ -330,21 +354,21 @@ int launch_align(const int32_t* ids, int64_t numel, int num_experts, int block_s
                      (long long)workspace_bytes, (long long)need);
   const int nchunks = static_cast<int>(std::max<int64_t>(1, cdiv(numel, kGridChunk)));
   int32_t* chunk_cnt = static_cast<int32_t*>(workspace);
-  int32_t* off = chunk_cnt + static_cast<int64_t>(nchunks) * num_experts;
   hipLaunchKernelGGL(align_count, dim3(nchunks), dim3(256), sizeof(int) * num_experts,
                      stream, ids, numel, kGridChunk, num_experts, emap, num_global,
                      chunk_cnt);
   XK_CHECK_LAUNCH("align_count");
-  hipLaunchKernelGGL(align_scan, dim3(1), dim3(1024),
-                     sizeof(int) * (2 * num_experts + 1 + 16 + 1024), stream, chunk_cnt,
-                     nchunks, num_experts, block_size, numel, max_pad, max_blocks,
-                     sorted_ids, expert_ids, num_post, expert_offsets, off);
-  XK_CHECK_LAUNCH("align_scan");
-  hipLaunchKernelGGL(align_scatter, dim3(nchunks), dim3(256),
-                     sizeof(int) * (2 * num_experts + 4 * (num_experts + 1)), stream, ids,
-                     numel, kGridChunk, num_experts, emap, num_global, chunk_cnt, off,
-                     sorted_ids);
-  XK_CHECK_LAUNCH("align_scatter");
+  {
+    const int threads = 1024, nw = threads / 64;
+    const int parts = std::max(1, threads / num_experts);
+    const size_t lds = sizeof(int) * (4 * num_experts + 1 + 16 + nw * (num_experts + 1) +
+                                      2 * parts * num_experts);
+    hipLaunchKernelGGL(align_place, dim3(nchunks), dim3(threads), lds, stream, ids, numel,
+                       kGridChunk, nchunks, num_experts, block_size, emap, num_global,
+                       chunk_cnt, max_pad, max_blocks, sorted_ids, expert_ids, num_post,
+                       expert_offsets);
+    XK_CHECK_LAUNCH("align_place");
+  }
   return XK_OK;
 }
 
