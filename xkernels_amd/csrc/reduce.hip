@@ -17,9 +17,11 @@ namespace xk {
 namespace {
 
 template <typename T, int VEC> struct vec_io;
+// Inputs are read exactly once: non-temporal loads keep them from displacing
+// useful cache lines (measured 192 -> 178 us on the [8192, 8, 7168] bf16 sum).
 template <> struct vec_io<uint16_t, 8> {
   __device__ __forceinline__ static void load(const uint16_t* p, float* v) {
-    const u32x4 r = *reinterpret_cast<const u32x4*>(p);
+    const u32x4 r = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       v[2 * i] = __uint_as_float(r[i] << 16);
@@ -37,8 +39,8 @@ template <> struct vec_io<uint16_t, 8> {
 };
 template <> struct vec_io<float, 8> {
   __device__ __forceinline__ static void load(const float* p, float* v) {
-    const f32x4 a = reinterpret_cast<const f32x4*>(p)[0];
-    const f32x4 b = reinterpret_cast<const f32x4*>(p)[1];
+    const f32x4 a = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p));
+    const f32x4 b = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p) + 1);
 #pragma unroll
     for (int i = 0; i < 4; ++i) { v[i] = a[i]; v[4 + i] = b[i]; }
   }
