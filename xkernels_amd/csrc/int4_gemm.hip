@@ -37,6 +37,12 @@
 
 #include "int4_common.h"
 
+#ifndef XK_INT4_STREAM_OCC
+#define XK_INT4_STREAM_OCC 2
+#endif
+#ifndef XK_INT4_SUPER
+#define XK_INT4_SUPER 8
+#endif
 #ifndef XK_INT4_STREAM_WAVES
 #define XK_INT4_STREAM_WAVES 4
 #endif
@@ -442,19 +448,21 @@ struct V2Args {
   int num_experts;
 };
 
-template <Int4Mode MODE, int WAVES>
-__global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
+template <Int4Mode MODE, int WAVES, int MAXNT>
+__global__ void __launch_bounds__(WAVES * 64)
+__attribute__((amdgpu_waves_per_eu(XK_INT4_STREAM_OCC, XK_INT4_STREAM_OCC)))
 int4_stream_v2(V2Args args) {
   constexpr bool kFast = MODE == Int4Mode::kFast;
   constexpr int kThreads = WAVES * 64;
   constexpr int kCols = WAVES * kColsPerWave;  // output columns per work item
   constexpr int kWRing = 4;       // weight chunks in registers (prefetch distance 3)
-  constexpr int kSuper = 8;       // chunks per scale superchunk: 64 groups = 128 B per row
-  constexpr int kSStride = 72;    // bf16 per scale row in LDS (128 B + 16 B pad)
-  __shared__ __attribute__((aligned(16))) uint16_t a_lds[2][kV2Rows * kV2Stride];
+  constexpr int kSuper = XK_INT4_SUPER;          // chunks per scale superchunk (8 groups each)
+  constexpr int kSStride = kSuper * 8 + 8;       // bf16 per scale row in LDS (16 B pad)
+  constexpr int kRowsPass = 16 * MAXNT;          // routed rows per pass
+  __shared__ __attribute__((aligned(16))) uint16_t a_lds[2][kRowsPass * kV2Stride];
   __shared__ __attribute__((aligned(16))) uint16_t s_lds[WAVES][2][32 * kSStride];
-  __shared__ int slot_lds[kV2Rows];
-  __shared__ int tok_lds[kV2Rows];
+  __shared__ int slot_lds[kRowsPass];
+  __shared__ int tok_lds[kRowsPass];
   const StreamArgs& p = args.s;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -481,10 +489,10 @@ int4_stream_v2(V2Args args) {
     const uint16_t* sp_src =
         p.scale + (static_cast<int64_t>(e) * N + min(n_base + sp_row, N - 1)) * G + sp_half * 4;
 
-    for (int pass = beg; pass < end; pass += kV2Rows) {
-      const int ntiles = min(2, (end - pass) >> 4);
+    for (int pass = beg; pass < end; pass += kRowsPass) {
+      const int ntiles = min(MAXNT, (end - pass) >> 4);
       __syncthreads();  // previous pass / item done with LDS
-      if (tid < kV2Rows) {
+      if (tid < kRowsPass) {
         int slot = -1, tok = -1;
         if (tid < ntiles * 16) {
           const int sidx = p.sorted_ids[pass + tid];
@@ -544,7 +552,7 @@ int4_stream_v2(V2Args args) {
       };
       // 8 bytes of scale superchunk `sc`, piece `pc` (16-byte slice of the row)
       auto load_spiece = [&](int sc, int pc) -> uint2 {
-        const int off = min(sc * 64 + pc * 8, G - 4);
+        const int off = min((sc * kSuper + pc) * 8, G - 4);
         return *reinterpret_cast<const uint2*>(sp_src + off);
       };
       // (index the __shared__ array directly: a pointer variable would turn
@@ -686,8 +694,8 @@ int4_stream_v2(V2Args args) {
         }
       }
       };
-      if (ntiles == 2)
-        body(std::integral_constant<int, 2>{});
+      if (MAXNT == 2 && ntiles == 2)
+        body(std::integral_constant<int, MAXNT>{});
       else
         body(std::integral_constant<int, 1>{});
     }
@@ -798,13 +806,24 @@ int launch_int4_gemm(const void* A, int a_dtype, int64_t M, int64_t K, const int
     if (K % 256 == 0 && a.scale_vec && !(flags & XK_INT4_V1)) {
       V2Args v2{a, int(E)};
       constexpr int kW = XK_INT4_STREAM_WAVES;
-      constexpr int kPerCu = kW == 8 ? 1 : 2;  // LDS of the scale superchunks limits residency
       const int64_t items = E * cdiv(N, kW * kColsPerWave);
-      const dim3 g2(static_cast<unsigned>(std::min<int64_t>(items, kPerCu * device_cu_count())));
-      if (flags & XK_INT4_FAST_DEQUANT)
-        hipLaunchKernelGGL((int4_stream_v2<Int4Mode::kFast, kW>), g2, dim3(kW * 64), 0, stream, v2);
-      else
-        hipLaunchKernelGGL((int4_stream_v2<Int4Mode::kRne, kW>), g2, dim3(kW * 64), 0, stream, v2);
+      // Few routed rows per expert (decode): 16-row passes, which halves the
+      // activation LDS; an expert with more rows takes several passes.
+      const bool one_tile = numel <= 16 * E;
+      const int per_cu = one_tile ? XK_INT4_STREAM_OCC : 2;
+      const dim3 g2(static_cast<unsigned>(std::min<int64_t>(items, per_cu * device_cu_count())));
+      const dim3 b2(kW * 64);
+      if (flags & XK_INT4_FAST_DEQUANT) {
+        if (one_tile)
+          hipLaunchKernelGGL((int4_stream_v2<Int4Mode::kFast, kW, 1>), g2, b2, 0, stream, v2);
+        else
+          hipLaunchKernelGGL((int4_stream_v2<Int4Mode::kFast, kW, 2>), g2, b2, 0, stream, v2);
+      } else {
+        if (one_tile)
+          hipLaunchKernelGGL((int4_stream_v2<Int4Mode::kRne, kW, 1>), g2, b2, 0, stream, v2);
+        else
+          hipLaunchKernelGGL((int4_stream_v2<Int4Mode::kRne, kW, 2>), g2, b2, 0, stream, v2);
+      }
       XK_CHECK_LAUNCH("int4_stream_v2");
       return XK_OK;
     }
