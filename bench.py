@@ -45,6 +45,8 @@ def parse() -> argparse.Namespace:
                     help="run warmup + timed steps only (for rocprofv3), print nothing else")
     ap.add_argument("--gemm-only", action="store_true",
                     help="with --profile-only: launch only the grouped GEMM (for --pmc passes)")
+    ap.add_argument("--extra-flags", type=int, default=0,
+                    help="diagnostic: XK_INT4_* bits OR-ed into the GEMM flags")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run 5 device copies of 1 GiB and exit (calibrates FETCH_SIZE/WRITE_SIZE)")
     return ap.parse_args()
@@ -85,6 +87,7 @@ def time_gemm_kernel(c, flags: int, iters: int) -> float:
     ws = torch.empty(max(1, _lib.query("xk_moe_align_workspace_bytes", numel, E)), dtype=torch.uint8, device=dev)
     parts = _lib.query("xk_moe_int4_gemm_parts", E, N, K, _lib.XK_DT_BF16, 32, flags)
     slot_out = torch.empty(parts, numel, N, dtype=torch.float32, device=dev)
+    gws = torch.empty(_lib.query("xk_moe_int4_gemm_workspace_bytes", M, K), dtype=torch.uint8, device=dev)
     stream = torch.cuda.current_stream()
     s = stream.cuda_stream
     _lib.call("xk_moe_align_block_size", c["ids"].data_ptr(), numel, E, bs, None, 0,
@@ -95,7 +98,7 @@ def time_gemm_kernel(c, flags: int, iters: int) -> float:
         _lib.call("xk_moe_int4_w4a16_gemm", c["A"].data_ptr(), _lib.XK_DT_BF16, M, K,
                   c["packed"].data_ptr(), c["scale"].data_ptr(), E, N, 32, c["ids"].data_ptr(),
                   top_k, None, 0, sorted_ids.data_ptr(), offsets.data_ptr(), slot_out.data_ptr(),
-                  flags, s)
+                  flags, gws.data_ptr(), gws.numel(), s)
 
     for _ in range(10):
         launch()
@@ -312,7 +315,7 @@ def main() -> int:
         return 0
     c = make_inputs(a.seed)
     exact = not a.fast_dequant
-    flags = 0 if exact else _lib.XK_INT4_FAST_DEQUANT
+    flags = (0 if exact else _lib.XK_INT4_FAST_DEQUANT) | a.extra_flags
     e_active = int(torch.unique(c["ids"]).numel())
     weight_bytes = int4_weight_bytes(e_active, c["N"], c["K"])
     ws = MoeInt4Workspace.allocate(c["M"], c["top_k"], c["N"], dtype=torch.bfloat16,

@@ -67,6 +67,9 @@ extern "C" {
  * kernel always uses the reference's bf16-rounded weights. */
 #define XK_INT4_FORCE_TILE 4
 #define XK_INT4_FORCE_STREAM 8
+/* Diagnostic: with XK_INT4_FAST_DEQUANT, use the column-split persistent
+ * stream kernel instead of the K-split decode kernel. */
+#define XK_INT4_V2 16
 
 /* Message of the last failed call on this thread ("" if none). */
 const char* xk_last_error(void);
@@ -134,11 +137,14 @@ int xk_moe_int4_w4a16(const void* A, int32_t a_dtype, int64_t M, int64_t K,
  * writes un-weighted fp32 per-slot rows for every routed slot (rows of dropped
  * slots are left untouched). The K range may be split: slot_out is
  * [parts, numel, N] with parts = xk_moe_int4_gemm_parts(...); the partial
- * planes are summed by xk_moe_topk_combine(..., nparts = parts). Used by
- * benchmarks to time the GEMM alone. */
+ * planes are summed by xk_moe_topk_combine(..., nparts = parts). The
+ * workspace (xk_moe_int4_gemm_workspace_bytes(M, K) bytes, 256-byte aligned)
+ * holds the fp16 activations XK_INT4_FAST_DEQUANT prepares; other modes do not
+ * touch it and accept NULL. Used by benchmarks to time the GEMM alone. */
 int32_t xk_moe_int4_block_size(int64_t M, int64_t top_k, int64_t E);
 int32_t xk_moe_int4_gemm_parts(int64_t E, int64_t N, int64_t K, int32_t a_dtype,
                                int32_t group_size, int32_t flags);
+int64_t xk_moe_int4_gemm_workspace_bytes(int64_t M, int64_t K);
 int xk_moe_int4_w4a16_gemm(const void* A, int32_t a_dtype, int64_t M, int64_t K,
                            const int32_t* packed, const uint16_t* scale,
                            int64_t E, int64_t N, int32_t group_size,
@@ -146,7 +152,8 @@ int xk_moe_int4_w4a16_gemm(const void* A, int32_t a_dtype, int64_t M, int64_t K,
                            const int32_t* expert_map, int32_t num_global_experts,
                            const int32_t* sorted_token_ids,
                            const int32_t* expert_offsets, float* slot_out,
-                           int32_t flags, hipStream_t stream);
+                           int32_t flags, void* workspace, int64_t workspace_bytes,
+                           hipStream_t stream);
 
 /* Stage entry point: the weighted top-k combine of per-slot fp32 rows,
  *   out[m, n] = sum_j valid(m,j) * [w[m,j]] * sum_p slot_out[p, m*top_k + j, n]

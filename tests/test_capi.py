@@ -38,7 +38,7 @@ def test_constants_match_header():
     d = _defines()
     for name in ("XK_OK", "XK_ERR_INVALID", "XK_ERR_WORKSPACE", "XK_ERR_LAUNCH", "XK_DT_BF16",
                  "XK_DT_FP32", "XK_DT_NONE", "XK_INT4_FAST_DEQUANT", "XK_INT4_V1",
-                 "XK_INT4_FORCE_TILE", "XK_INT4_FORCE_STREAM"):
+                 "XK_INT4_FORCE_TILE", "XK_INT4_FORCE_STREAM", "XK_INT4_V2"):
         assert getattr(_lib, name) == d[name], name
 
 
@@ -123,14 +123,18 @@ def test_int4_rejects_bad_arguments():
 def test_int4_gemm_stage_rejects_bad_arguments():
     def g(**kw):
         a = dict(A=FAKE, dt=0, M=4, K=64, packed=FAKE, scale=FAKE, E=2, N=16, gs=32, ids=FAKE, k=2,
-                 emap=None, ng=0, s=FAKE, off=FAKE, out=FAKE, flags=0, stream=None)
+                 emap=None, ng=0, s=FAKE, off=FAKE, out=FAKE, flags=0, ws=None, wsb=0, stream=None)
         a.update(kw)
         return _rc("xk_moe_int4_w4a16_gemm", a["A"], a["dt"], a["M"], a["K"], a["packed"], a["scale"],
                    a["E"], a["N"], a["gs"], a["ids"], a["k"], a["emap"], a["ng"], a["s"], a["off"],
-                   a["out"], a["flags"], a["stream"])
+                   a["out"], a["flags"], a["ws"], a["wsb"], a["stream"])
     assert g(K=60) == _lib.XK_ERR_INVALID
     assert g(gs=48) == _lib.XK_ERR_INVALID
     assert g(dt=3) == _lib.XK_ERR_INVALID
+    # the FAST mode needs the activation workspace (K a multiple of 256)
+    assert g(K=256, flags=_lib.XK_INT4_FAST_DEQUANT) == _lib.XK_ERR_WORKSPACE
+    assert g(K=256, flags=_lib.XK_INT4_FAST_DEQUANT, ws=FAKE,
+             wsb=_lib.query("xk_moe_int4_gemm_workspace_bytes", 4, 256) - 1) == _lib.XK_ERR_WORKSPACE
 
 
 def test_combine_rejects_bad_arguments():

@@ -58,7 +58,7 @@ def _slot_rows(A, packed, scale, ids, flags):
     slot_out = torch.full((1, numel, N), float("nan"), dtype=torch.float32, device=dev)
     _lib.call("xk_moe_int4_w4a16_gemm", A.data_ptr(), _lib.XK_DT_BF16, M, K, packed.data_ptr(),
               scale.data_ptr(), E, N, 32, ids.data_ptr(), k, None, 0, sorted_ids.data_ptr(),
-              offsets.data_ptr(), slot_out.data_ptr(), flags, _stream())
+              offsets.data_ptr(), slot_out.data_ptr(), flags, None, 0, _stream())
     return slot_out[0]
 
 

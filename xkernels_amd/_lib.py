@@ -24,6 +24,7 @@ XK_INT4_FAST_DEQUANT = 1
 XK_INT4_V1 = 2
 XK_INT4_FORCE_TILE = 4
 XK_INT4_FORCE_STREAM = 8
+XK_INT4_V2 = 16
 
 _p = ctypes.c_void_p
 _i32 = ctypes.c_int32
@@ -49,8 +50,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "xk_moe_int4_block_size": (_i32, [_i64, _i64, _i64]),
     "xk_moe_int4_w4a16_gemm": (
         ctypes.c_int,
-        [_p, _i32, _i64, _i64, _p, _p, _i64, _i64, _i32, _p, _i64, _p, _i32, _p, _p, _p, _i32, _p],
+        [_p, _i32, _i64, _i64, _p, _p, _i64, _i64, _i32, _p, _i64, _p, _i32, _p, _p, _p, _i32, _p,
+         _i64, _p],
     ),
+    "xk_moe_int4_gemm_workspace_bytes": (_i64, [_i64, _i64]),
     "xk_moe_topk_combine": (
         ctypes.c_int,
         [_p, _i64, _i64, _i64, _p, _i32, _p, _i32, _p, _i32, _p, _i32, _i32, _p],

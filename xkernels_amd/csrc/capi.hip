@@ -40,11 +40,13 @@ int launch_topk_combine(const float* slot_out, int64_t M, int64_t top_k, int64_t
 int int4_gemm_parts(int64_t E, int64_t N, int64_t K, int a_dtype, int group_size, int flags);
 int int4_block_size();
 bool int4_use_stream(int a_dtype, int group_size, int64_t K);
+int64_t int4_gemm_workspace_bytes(int64_t M, int64_t K);
 int launch_int4_gemm(const void* A, int a_dtype, int64_t M, int64_t K, const int32_t* packed,
                      const uint16_t* scale, int64_t E, int64_t N, int group_size,
                      const int32_t* topk_ids, int64_t top_k, const int32_t* emap,
                      int num_global, const int32_t* sorted_ids, const int32_t* offsets,
-                     float* slot_out, int flags, hipStream_t stream);
+                     float* slot_out, int flags, void* workspace, int64_t workspace_bytes,
+                     hipStream_t stream);
 int mxfp4_block_size();
 int launch_mxfp4_stage(int stage, const void* A, int a_dtype, const uint8_t* w,
                        const uint8_t* ws, const uint16_t* bias, int64_t E, int64_t K,
@@ -135,7 +137,11 @@ int64_t xk_moe_int4_w4a16_workspace_bytes(int64_t M, int64_t top_k, int64_t E, i
   AlignScratch al(numel, int(E), int4_block_size());
   // sized for the largest number of partial planes any mode / dtype uses
   const int64_t parts = int4_gemm_parts(E, N, K, XK_DT_BF16, 32, 0);
-  return al.total + round_up(parts * numel * N * 4);
+  return al.total + round_up(parts * numel * N * 4) + round_up(int4_gemm_workspace_bytes(M, K));
+}
+
+int64_t xk_moe_int4_gemm_workspace_bytes(int64_t M, int64_t K) {
+  return int4_gemm_workspace_bytes(M, K);
 }
 
 int xk_moe_int4_w4a16_gemm(const void* A, int32_t a_dtype, int64_t M, int64_t K,
@@ -143,11 +149,12 @@ int xk_moe_int4_w4a16_gemm(const void* A, int32_t a_dtype, int64_t M, int64_t K,
                            int32_t group_size, const int32_t* topk_ids, int64_t top_k,
                            const int32_t* expert_map, int32_t num_global_experts,
                            const int32_t* sorted_token_ids, const int32_t* expert_offsets,
-                           float* slot_out, int32_t flags, hipStream_t stream) {
+                           float* slot_out, int32_t flags, void* workspace,
+                           int64_t workspace_bytes, hipStream_t stream) {
   clear_error();
   return launch_int4_gemm(A, a_dtype, M, K, packed, scale, E, N, group_size, topk_ids, top_k,
                           expert_map, num_global_experts, sorted_token_ids, expert_offsets,
-                          slot_out, flags, stream);
+                          slot_out, flags, workspace, workspace_bytes, stream);
 }
 
 int xk_moe_topk_combine(const float* slot_out, int64_t M, int64_t top_k, int64_t N,
@@ -182,6 +189,7 @@ int xk_moe_int4_w4a16(const void* A, int32_t a_dtype, int64_t M, int64_t K,
   const int64_t numel = M * top_k;
   AlignScratch al(numel, int(E), int4_block_size());
   float* slot_out = at<float>(workspace, al.total);
+  const int64_t gemm_ws = al.total + round_up(int4_gemm_parts(E, N, K, XK_DT_BF16, 32, 0) * numel * N * 4);
   const int32_t* sorted = nullptr;
   const int32_t* offsets = nullptr;
   if (int4_use_stream(a_dtype, group_size, K)) {
@@ -197,7 +205,8 @@ int xk_moe_int4_w4a16(const void* A, int32_t a_dtype, int64_t M, int64_t K,
   }
   if (int rc = launch_int4_gemm(A, a_dtype, M, K, packed, scale, E, N, group_size, topk_ids,
                                 top_k, expert_map, num_global_experts, sorted, offsets,
-                                slot_out, flags, stream))
+                                slot_out, flags, at<char>(workspace, gemm_ws),
+                                round_up(int4_gemm_workspace_bytes(M, K)), stream))
     return rc;
   return launch_topk_combine(slot_out, M, top_k, N, topk_w, mul_routed_weight, topk_ids,
                              int(E), expert_map, num_global_experts, out, a_dtype,

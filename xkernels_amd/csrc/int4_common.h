@@ -78,6 +78,16 @@ __device__ __forceinline__ bf16x8 dequant_rne(uint32_t w, const RneScale& k, uin
   return __builtin_bit_cast(bf16x8, b);
 }
 
+// 8 nibbles -> fp16 in dequant_rne's element order n0 n4 n1 n5 n2 n6 n3 n7:
+// pairs (n0, n4) and (n2, n6) read 1024 + n, pairs (n1, n5) and (n3, n7) read
+// 1024 + 16 n (one v_and_or_b32 per pair, one shift per word). The contraction
+// partner must carry 1/16 at the second kind of position.
+__device__ __forceinline__ u32x4 unpack_f16(uint32_t w, uint32_t mlo, uint32_t mhi) {
+  const uint32_t w8 = w >> 8;
+  return u32x4{and_or(w, mlo, 0x64006400u), and_or(w, mhi, 0x64006400u),
+               and_or(w8, mlo, 0x64006400u), and_or(w8, mhi, 0x64006400u)};
+}
+
 // 8 nibbles -> bf16 (128 + n), same element order as dequant_rne.
 __device__ __forceinline__ bf16x8 dequant_magic(uint32_t w, uint32_t mask) {
   u32x4 b;
@@ -85,6 +95,15 @@ __device__ __forceinline__ bf16x8 dequant_magic(uint32_t w, uint32_t mask) {
   for (int d = 0; d < 4; ++d) b[d] = and_or(w >> (4 * d), mask, 0x43004300u);
   return __builtin_bit_cast(bf16x8, b);
 }
+
+// Activations prepared for the FAST INT4 kernels (int4_prep_a): fp16 rows in
+// the unpack's k order, a power-of-two exponent per row, and per row and
+// quantisation group the sum that cancels the unpack's 1024 offsets.
+struct Int4Prep {
+  uint16_t* a16;   // [M, K] fp16
+  int32_t* a_exp;  // [M]
+  float* a_corr;   // [M, K / 32]
+};
 
 // Persistent kernels enumerate work over the experts that received slots:
 // the padded align offsets give each expert's range; empty experts are skipped.

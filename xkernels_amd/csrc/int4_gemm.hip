@@ -40,9 +40,6 @@
 #ifndef XK_INT4_STREAM_OCC
 #define XK_INT4_STREAM_OCC 2
 #endif
-#ifndef XK_INT4_SUPER
-#define XK_INT4_SUPER 8
-#endif
 #ifndef XK_INT4_STREAM_WAVES
 #define XK_INT4_STREAM_WAVES 4
 #endif
@@ -424,20 +421,26 @@ int4_stream_gemm_rne(StreamArgs p) {
 //     ahead); activations go through two LDS buffers (one barrier per chunk);
 //     every global load is unconditional (clamped indices) so the compiler can
 //     count outstanding loads instead of draining them;
-//   * group scales arrive in full 128-byte lines: each wave keeps a
-//     double-buffered LDS copy of its 32 rows' scales for 8 chunks, refilled
-//     8 bytes per lane per chunk (fetching a scale line piecewise per chunk
-//     lets the weight stream evict it between visits);
+//   * every load a step consumes (weights of chunk c, activations of chunk
+//     c+1, the scale piece of chunk c+8) was issued three steps earlier and in
+//     the same step: loads return in issue order, so a wait for a load issued
+//     later than the weights it follows would drain the weight ring;
+//   * group scales: each wave keeps its 32 rows' scales for 16 chunks in an
+//     LDS ring (16 bytes per row and chunk), refilled 8 bytes per lane per
+//     step, 8 chunks ahead of use;
 //   * activations are staged with the k-permutation the nibble unpack
 //     produces and a 544-byte row pitch, so the MFMA operand reads are
 //     bank-conflict free;
 //   * RNE mode dequantises every weight to bf16_rne((n-8)*s) before the MFMA
-//     (reference rounding). FAST mode transposes the four words of a group
-//     across the four lane groups with v_permlane32_swap / v_permlane16_swap
-//     so one MFMA contracts one group, unpacks nibbles to bf16 (128+n) with
-//     v_and_or_b32, subtracts 136*sum(a) with a second MFMA against a constant
-//     -136 operand (shared by both column tiles) and applies the group scale
-//     to the MFMA result.
+//     (reference rounding). FAST mode contracts in fp16 against activations
+//     prepared by int4_prep_a (fp16, exact per-row power-of-two scale, the
+//     unpack's k order, 1/16 at the 16n positions): it transposes the four
+//     words of a group across the four lane groups with v_permlane32_swap /
+//     v_permlane16_swap so one MFMA contracts one group, unpacks nibbles to
+//     fp16 1024+n / 1024+16n with one v_and_or_b32 per pair, removes the
+//     offsets with a second MFMA against a constant operand (shared by both
+//     column tiles) and applies the group scale to the MFMA result. The
+//     weights are then exact (n-8)*s rather than bf16-rounded.
 enum class Int4Mode { kRne, kFast };
 
 constexpr int kV2Rows = 32;  // two 16-row MFMA tiles per pass
@@ -446,6 +449,7 @@ constexpr int kV2Stride = kChunkK + 16;  // bf16 per LDS row: 544 B, bank-stagge
 struct V2Args {
   StreamArgs s;
   int num_experts;
+  const int32_t* a_exp;  // FAST: per-token power-of-two exponent of the prepared A
 };
 
 template <Int4Mode MODE, int WAVES, int MAXNT>
@@ -455,14 +459,15 @@ int4_stream_v2(V2Args args) {
   constexpr bool kFast = MODE == Int4Mode::kFast;
   constexpr int kThreads = WAVES * 64;
   constexpr int kCols = WAVES * kColsPerWave;  // output columns per work item
-  constexpr int kWRing = 4;       // weight chunks in registers (prefetch distance 3)
-  constexpr int kSuper = XK_INT4_SUPER;          // chunks per scale superchunk (8 groups each)
-  constexpr int kSStride = kSuper * 8 + 8;       // bf16 per scale row in LDS (16 B pad)
+  constexpr int kRing = 4;         // register ring depth (loads issued 3 steps ahead)
+  constexpr int kSSlots = 16;      // scale LDS ring: chunks held per row
+  constexpr int kSStride = kSSlots * 8 + 8;      // bf16 per scale row in LDS (16 B pad)
   constexpr int kRowsPass = 16 * MAXNT;          // routed rows per pass
   __shared__ __attribute__((aligned(16))) uint16_t a_lds[2][kRowsPass * kV2Stride];
-  __shared__ __attribute__((aligned(16))) uint16_t s_lds[WAVES][2][32 * kSStride];
+  __shared__ __attribute__((aligned(16))) uint16_t s_lds[WAVES][32 * kSStride];
   __shared__ int slot_lds[kRowsPass];
   __shared__ int tok_lds[kRowsPass];
+  __shared__ int exp_lds[kRowsPass];
   const StreamArgs& p = args.s;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -472,7 +477,9 @@ int4_stream_v2(V2Args args) {
   const int nchunks = G / kChunkGroups;
   const int items = count_active_experts(p.offsets, args.num_experts) * nb;
   const uint32_t kNibMask = in_vgpr(0x000F000Fu), kNibMaskHi = in_vgpr(0x00F000F0u);
-  const bf16x8 neg136 = __builtin_bit_cast(bf16x8, u32x4{0xC308C308u, 0xC308C308u, 0xC308C308u, 0xC308C308u});
+  typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+  // -1032 at the 1024 + n positions, -1152 (= 16 * 72) at the 1024 + 16n ones
+  const f16x8 negc = __builtin_bit_cast(f16x8, u32x4{0xE408E408u, 0xE480E480u, 0xE408E408u, 0xE480E480u});
 
   for (int item = blockIdx.x; item < items; item += gridDim.x) {
     const int e = find_active_expert(p.offsets, args.num_experts, item / nb);
@@ -500,6 +507,7 @@ int4_stream_v2(V2Args args) {
         }
         slot_lds[tid] = slot;
         tok_lds[tid] = tok;
+        if constexpr (kFast) exp_lds[tid] = tok >= 0 ? args.a_exp[tok] : 0;
       }
       __syncthreads();
       // The pass body is compiled for one and for two 16-row tiles, so that
@@ -532,14 +540,20 @@ int4_stream_v2(V2Args args) {
         //   FAST: (g >> 2) * 64 + (g & 3) * 16 + j * 4   (lane q reads subgroup q)
         // so the 16-byte reads of one MFMA are 4 dwords apart across lane groups
         // and the 16 rows are 136 dwords apart: bank-conflict free.
+        // FAST: the prepared activations are already in this order (group g at
+        // dword 16 g, subgroup j at + 4 j) and are copied as they are.
         uint32_t* row = reinterpret_cast<uint32_t*>(&a_lds[buf][st_r * kV2Stride]);
 #pragma unroll
         for (int i = 0; i < kVec; ++i) {
-          uint32_t in[4] = {ar[i][0], ar[i][1], ar[i][2], ar[i][3]}, o[4];
-          perm8(in, o);
           const int g = (v0 + i) >> 2, j = (v0 + i) & 3;
-          const int off = (g >> 2) * 64 + (kFast ? (g & 3) * 16 + j * 4 : j * 16 + (g & 3) * 4);
-          *reinterpret_cast<u32x4*>(row + off) = u32x4{o[0], o[1], o[2], o[3]};
+          if constexpr (kFast) {
+            *reinterpret_cast<u32x4*>(row + 4 * (v0 + i)) = ar[i];
+          } else {
+            uint32_t in[4] = {ar[i][0], ar[i][1], ar[i][2], ar[i][3]}, o[4];
+            perm8(in, o);
+            const int off = (g >> 2) * 64 + j * 16 + (g & 3) * 4;
+            *reinterpret_cast<u32x4*>(row + off) = u32x4{o[0], o[1], o[2], o[3]};
+          }
         }
       };
       auto load_w = [&](int chunk, u32x4 (&wr)[2][2]) {
@@ -550,15 +564,15 @@ int4_stream_v2(V2Args args) {
           for (int h = 0; h < 2; ++h)
             wr[c][h] = *reinterpret_cast<const u32x4*>(wrow[c] + (chunk * kChunkGroups + 4 * h) * 4);
       };
-      // 8 bytes of scale superchunk `sc`, piece `pc` (16-byte slice of the row)
-      auto load_spiece = [&](int sc, int pc) -> uint2 {
-        const int off = min((sc * kSuper + pc) * 8, G - 4);
-        return *reinterpret_cast<const uint2*>(sp_src + off);
+      // this lane's 8 bytes of the scales of chunk `chunk` (8 groups per row)
+      auto load_spiece = [&](int chunk) -> uint2 {
+        return *reinterpret_cast<const uint2*>(sp_src + min(chunk, nchunks - 1) * 8);
       };
       // (index the __shared__ array directly: a pointer variable would turn
       // these into flat accesses, which also count as vector-memory loads)
-      auto store_spiece = [&](int sc, int pc, uint2 v) {
-        *reinterpret_cast<uint2*>(&s_lds[wave][sc & 1][sp_row * kSStride + pc * 8 + sp_half * 4]) = v;
+      auto store_spiece = [&](int chunk, uint2 v) {
+        *reinterpret_cast<uint2*>(
+            &s_lds[wave][sp_row * kSStride + (chunk % kSSlots) * 8 + sp_half * 4]) = v;
       };
 
       f32x4 acc[2][2];
@@ -570,11 +584,10 @@ int4_stream_v2(V2Args args) {
       auto compute = [&](int buf, int chunk, const u32x4 (&wr)[2][2]) {
         // the chunk's 8 group scales of both column rows
         uint32_t sr[2][4];
-        const int sbuf = (chunk / kSuper) & 1;
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
           const u32x4 v = *reinterpret_cast<const u32x4*>(
-              &s_lds[wave][sbuf][(16 * c + c16) * kSStride + (chunk % kSuper) * 8]);
+              &s_lds[wave][(16 * c + c16) * kSStride + (chunk % kSSlots) * 8]);
 #pragma unroll
           for (int i = 0; i < 4; ++i) sr[c][i] = v[i];
         }
@@ -586,24 +599,24 @@ int4_stream_v2(V2Args args) {
             for (int c = 0; c < 2; ++c) { w[c] = wr[c][h]; transpose4(w[c]); }
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-              bf16x8 bfrag[2];
+              f16x8 bfrag[2];
               float sc[2];
 #pragma unroll
               for (int c = 0; c < 2; ++c) {
-                bfrag[c] = dequant_magic(w[c][j], kNibMask);
+                bfrag[c] = __builtin_bit_cast(f16x8, unpack_f16(w[c][j], kNibMask, kNibMaskHi));
                 const uint32_t sw = sr[c][(4 * h + j) >> 1];
                 sc[c] = __uint_as_float(((4 * h + j) & 1) ? (sw & 0xFFFF0000u) : (sw << 16));
               }
 #pragma unroll
               for (int t = 0; t < 2; ++t) {
                 if (t >= NT) break;
-                const bf16x8 afrag = *reinterpret_cast<const bf16x8*>(
+                const f16x8 afrag = *reinterpret_cast<const f16x8*>(
                     &a_lds[buf][(t * 16 + c16) * kV2Stride + 2 * (h * 64 + j * 16 + q * 4)]);
-                const f32x4 d2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                    afrag, neg136, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                const f32x4 d2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                    afrag, negc, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
 #pragma unroll
                 for (int c = 0; c < 2; ++c) {
-                  const f32x4 d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(afrag, bfrag[c], d2, 0, 0, 0);
+                  const f32x4 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(afrag, bfrag[c], d2, 0, 0, 0);
 #pragma unroll
                   for (int i = 0; i < 4; ++i) acc[t][c][i] = fmaf(sc[c], d[i], acc[t][c][i]);
                 }
@@ -636,47 +649,52 @@ int4_stream_v2(V2Args args) {
         }
       };
 
-      // Prologue: scale superchunk 0 and activation chunk 0 in LDS, A(1) and
-      // W(0..2) in flight.
-      u32x4 areg[kVec];
+      // Register ring slot r holds, after step c with c % 4 == r, the loads
+      // issued at that step: activations of chunk c+4 and the scale piece of
+      // chunk c+11 (weights: chunk c+3 in slot (c+3) % 4).
+      struct Stage {
+        u32x4 a[kVec];
+        uint2 sp;
+      };
+      Stage r0, r1, r2, r3;
       u32x4 w0[2][2], w1[2][2], w2[2][2], w3[2][2];
-#pragma unroll
-      for (int pc = 0; pc < kSuper; ++pc) store_spiece(0, pc, load_spiece(0, pc));
-      load_a(0, areg);
-      store_a(0, areg);
-      // Issue the rest in the order the loop leaves its loads outstanding at
-      // its head (W(c+1), A(c+1), W(c+2)): the load-counter wait the compiler
-      // derives at the loop head covers both paths into it, and a prologue
-      // that ends with the activation loads would make it a full drain.
-      __builtin_amdgcn_sched_barrier(0);
-      load_w(0, w0);
-      __builtin_amdgcn_sched_barrier(0);
-      load_w(1, w1);
-      __builtin_amdgcn_sched_barrier(0);
-      load_a(1, areg);
-      __builtin_amdgcn_sched_barrier(0);
-      load_w(2, w2);
-      __builtin_amdgcn_sched_barrier(0);
-      uint2 spiece = make_uint2(0u, 0u);
-      // step c: A(c+1) -> LDS buffer (c+1)&1 (freed by compute(c-1)); the scale
-      // piece loaded at step c-1 -> LDS; request A(c+2), scale piece (c/8+1, c%8)
-      // and W(c+3); compute chunk c.
-      auto step = [&](int c, const u32x4 (&wc)[2][2], u32x4 (&wn)[2][2]) {
-        __syncthreads();
-        store_a((c + 1) & 1, areg);
-        // LDS operations of one wave execute in order, so the other lanes'
-        // reads in compute() see this piece without a barrier.
-        if (c > 0) store_spiece((c - 1) / kSuper + 1, (c - 1) % kSuper, spiece);
-        load_a(c + 2, areg);
-        spiece = load_spiece(c / kSuper + 1, c % kSuper);
+      auto issue = [&](int c, Stage& st, u32x4 (&wn)[2][2]) {
+        load_a(c + 4, st.a);
+        st.sp = load_spiece(c + 11);
         load_w(c + 3, wn);
+      };
+      // Prologue: scales of chunks 0-7 and activations of chunk 0 in LDS, then
+      // the loads of the three steps "before" step 0, in the loop's order, so
+      // the load-counter wait at the loop head is the same on both paths.
+#pragma unroll
+      for (int ch = 0; ch < 8; ++ch) store_spiece(ch, load_spiece(ch));
+      load_a(0, r0.a);
+      store_a(0, r0.a);
+      __builtin_amdgcn_sched_barrier(0);
+      issue(-3, r1, w0);
+      __builtin_amdgcn_sched_barrier(0);
+      issue(-2, r2, w1);
+      __builtin_amdgcn_sched_barrier(0);
+      issue(-1, r3, w2);
+      __builtin_amdgcn_sched_barrier(0);
+      // step c: A(c+1) -> LDS buffer (c+1)&1 (freed by compute(c-1)) and the
+      // scale piece of chunk c+8 -> its ring slot (last read at step c-8), both
+      // from ring slot (c+1) % 4; issue step c's loads into slot c % 4 and
+      // W(c+3); compute chunk c. LDS operations of one wave execute in order,
+      // so the other lanes' scale reads see the piece without a barrier.
+      auto step = [&](int c, const u32x4 (&wc)[2][2], u32x4 (&wn)[2][2], const Stage& st,
+                      Stage& ld) {
+        __syncthreads();
+        store_a((c + 1) & 1, st.a);
+        store_spiece(c + 8, st.sp);
+        issue(c, ld, wn);
         if (c < nchunks) compute(c & 1, c, wc);
       };
-      for (int c = 0; c < nchunks; c += kWRing) {
-        step(c, w0, w3);
-        step(c + 1, w1, w0);
-        step(c + 2, w2, w1);
-        step(c + 3, w3, w2);
+      for (int c = 0; c < nchunks; c += kRing) {
+        step(c, w0, w3, r1, r0);
+        step(c + 1, w1, w0, r2, r1);
+        step(c + 2, w2, w1, r3, r2);
+        step(c + 3, w3, w2, r0, r3);
       }
 
 #pragma unroll
@@ -686,10 +704,12 @@ int4_stream_v2(V2Args args) {
         for (int i = 0; i < 4; ++i) {
           const int slot = slot_lds[t * 16 + q * 4 + i];
           if (slot < 0) continue;
+          const int ex = kFast ? exp_lds[t * 16 + q * 4 + i] : 0;
 #pragma unroll
           for (int c = 0; c < 2; ++c) {
             const int n = n_base + 16 * c + c16;
-            if (n < N) p.out[static_cast<int64_t>(slot) * N + n] = acc[t][c][i];
+            const float v = kFast ? ldexpf(acc[t][c][i], ex) : acc[t][c][i];
+            if (n < N) p.out[static_cast<int64_t>(slot) * N + n] = v;
           }
         }
       }
@@ -767,6 +787,8 @@ int int4_gemm_parts(int64_t E, int64_t N, int64_t K, int a_dtype, int group_size
 }
 
 bool int4_prefill_ok(int a_dtype, int group_size, int64_t K, int64_t N, int64_t E);
+bool int4_ksplit_ok(int64_t K, int64_t N, int64_t E, int64_t numel);
+
 int launch_int4_prefill(const void* A, int64_t K, const int32_t* packed, const uint16_t* scale,
                         int64_t E, int64_t N, int64_t numel, int64_t top_k,
                         const int32_t* sorted_ids, const int32_t* offsets, float* slot_out,
@@ -776,11 +798,22 @@ int launch_int4_prefill(const void* A, int64_t K, const int32_t* packed, const u
 // weight-streaming kernel.
 constexpr int64_t kPrefillRowsPerExpert = 64;
 
+// FAST-mode activation preparation (int4_decode.hip): scratch layout and launch.
+int64_t int4_gemm_workspace_bytes(int64_t M, int64_t K);
+Int4Prep int4_prep_layout(void* workspace, int64_t M, int64_t K);
+int launch_int4_prep(const uint16_t* A, int64_t M, int64_t K, const Int4Prep& prep,
+                     hipStream_t stream);
+int launch_int4_ksplit(const Int4Prep& prep, int64_t K, const int32_t* packed,
+                       const uint16_t* scale, int64_t E, int64_t N, int64_t numel, int64_t top_k,
+                       const int32_t* sorted_ids, const int32_t* offsets, float* slot_out,
+                       hipStream_t stream);
+
 int launch_int4_gemm(const void* A, int a_dtype, int64_t M, int64_t K, const int32_t* packed,
                      const uint16_t* scale, int64_t E, int64_t N, int group_size,
                      const int32_t* topk_ids, int64_t top_k, const int32_t* emap,
                      int num_global, const int32_t* sorted_ids, const int32_t* offsets,
-                     float* slot_out, int flags, hipStream_t stream) {
+                     float* slot_out, int flags, void* workspace, int64_t workspace_bytes,
+                     hipStream_t stream) {
   XK_REQUIRE(a_dtype == XK_DT_BF16 || a_dtype == XK_DT_FP32, "int4: bad A dtype %d", a_dtype);
   XK_REQUIRE(M >= 0 && top_k >= 1 && E >= 1 && N >= 1 && K >= 8, "int4: bad sizes");
   XK_REQUIRE(K % 8 == 0, "int4: K=%lld not a multiple of 8", (long long)K);
@@ -804,7 +837,7 @@ int launch_int4_gemm(const void* A, int a_dtype, int64_t M, int64_t K, const int
                  scale, sorted_ids, offsets, slot_out, int(K), int(N), int(numel), int(top_k),
                  int((K / 32) % 8 == 0 && reinterpret_cast<uintptr_t>(scale) % 16 == 0)};
     if (K % 256 == 0 && a.scale_vec && !(flags & XK_INT4_V1)) {
-      V2Args v2{a, int(E)};
+      V2Args v2{a, int(E), nullptr};
       constexpr int kW = XK_INT4_STREAM_WAVES;
       const int64_t items = E * cdiv(N, kW * kColsPerWave);
       // Few routed rows per expert (decode): 16-row passes, which halves the
@@ -814,6 +847,19 @@ int launch_int4_gemm(const void* A, int a_dtype, int64_t M, int64_t K, const int
       const dim3 g2(static_cast<unsigned>(std::min<int64_t>(items, per_cu * device_cu_count())));
       const dim3 b2(kW * 64);
       if (flags & XK_INT4_FAST_DEQUANT) {
+        const int64_t need = int4_gemm_workspace_bytes(M, K);
+        if (workspace == nullptr || workspace_bytes < need)
+          return set_error(XK_ERR_WORKSPACE, "int4 gemm: workspace %lld B < %lld B",
+                           (long long)workspace_bytes, (long long)need);
+        XK_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 256 == 0,
+                   "int4 gemm: workspace must be 256-byte aligned");
+        const Int4Prep prep = int4_prep_layout(workspace, M, K);
+        if (int rc = launch_int4_prep(static_cast<const uint16_t*>(A), M, K, prep, stream)) return rc;
+        v2.s.A = prep.a16;
+        v2.a_exp = prep.a_exp;
+        if (one_tile && int4_ksplit_ok(K, N, E, numel) && !(flags & XK_INT4_V2))
+          return launch_int4_ksplit(prep, K, packed, scale, E, N, numel, top_k, sorted_ids,
+                                    offsets, slot_out, stream);
         if (one_tile)
           hipLaunchKernelGGL((int4_stream_v2<Int4Mode::kFast, kW, 1>), g2, b2, 0, stream, v2);
         else
