@@ -85,7 +85,7 @@ def time_gemm_kernel(c, flags: int, iters: int) -> float:
     num_post = torch.empty(1, dtype=torch.int32, device=dev)
     offsets = torch.empty(E + 1, dtype=torch.int32, device=dev)
     ws = torch.empty(max(1, _lib.query("xk_moe_align_workspace_bytes", numel, E)), dtype=torch.uint8, device=dev)
-    parts = _lib.query("xk_moe_int4_gemm_parts", E, N, K, _lib.XK_DT_BF16, 32, flags)
+    parts = _lib.query("xk_moe_int4_gemm_parts", M, top_k, E, N, K, _lib.XK_DT_BF16, 32, flags)
     slot_out = torch.empty(parts, numel, N, dtype=torch.float32, device=dev)
     gws = torch.empty(_lib.query("xk_moe_int4_gemm_workspace_bytes", M, K), dtype=torch.uint8, device=dev)
     stream = torch.cuda.current_stream()

@@ -133,17 +133,20 @@ int xk_moe_int4_w4a16(const void* A, int32_t a_dtype, int64_t M, int64_t K,
 
 /* Stage entry point: only the grouped INT4 GEMM (the reference's
  * _fused_moe_int4_kernel launch, moe_int4_kernel.py:78-272). Consumes the
- * align outputs built with block_size = xk_moe_int4_block_size(M, top_k, E) and
- * writes un-weighted fp32 per-slot rows for every routed slot (rows of dropped
- * slots are left untouched). The K range may be split: slot_out is
- * [parts, numel, N] with parts = xk_moe_int4_gemm_parts(...); the partial
- * planes are summed by xk_moe_topk_combine(..., nparts = parts). The
- * workspace (xk_moe_int4_gemm_workspace_bytes(M, K) bytes, 256-byte aligned)
- * holds the fp16 activations XK_INT4_FAST_DEQUANT prepares; other modes do not
- * touch it and accept NULL. Used by benchmarks to time the GEMM alone. */
+ * align outputs built with block_size = xk_moe_int4_block_size(M, top_k, E)
+ * (expert_offsets are multiples of that block size) and writes un-weighted
+ * fp32 per-slot rows for every routed slot (rows of dropped slots are left
+ * untouched). The decode kernel splits K: slot_out is [parts, numel, N] with
+ * parts = xk_moe_int4_gemm_parts(...) for the same arguments; every plane
+ * holds one K slice's partial rows and xk_moe_topk_combine(..., nparts =
+ * parts) sums them. The workspace (xk_moe_int4_gemm_workspace_bytes(M, K)
+ * bytes, 256-byte aligned) holds the fp16 activations XK_INT4_FAST_DEQUANT
+ * prepares; other modes do not touch it and accept NULL. A, packed and scale
+ * must be 16-byte aligned for the MFMA kernels. Used by benchmarks to time
+ * the GEMM alone. */
 int32_t xk_moe_int4_block_size(int64_t M, int64_t top_k, int64_t E);
-int32_t xk_moe_int4_gemm_parts(int64_t E, int64_t N, int64_t K, int32_t a_dtype,
-                               int32_t group_size, int32_t flags);
+int32_t xk_moe_int4_gemm_parts(int64_t M, int64_t top_k, int64_t E, int64_t N, int64_t K,
+                               int32_t a_dtype, int32_t group_size, int32_t flags);
 int64_t xk_moe_int4_gemm_workspace_bytes(int64_t M, int64_t K);
 int xk_moe_int4_w4a16_gemm(const void* A, int32_t a_dtype, int64_t M, int64_t K,
                            const int32_t* packed, const uint16_t* scale,

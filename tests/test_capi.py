@@ -55,7 +55,7 @@ def _pad(numel, E, bs):
 def test_size_queries():
     bs = _lib.query("xk_moe_int4_block_size", 64, 8, 48)
     assert bs >= 1
-    assert _lib.query("xk_moe_int4_gemm_parts", 48, 4096, 7168, _lib.XK_DT_BF16, 32, 0) >= 1
+    assert _lib.query("xk_moe_int4_gemm_parts", 64, 8, 48, 4096, 7168, _lib.XK_DT_BF16, 32, 0) >= 1
     assert _lib.query("xk_moe_align_workspace_bytes", 512, 48) >= 0
     ws = _lib.query("xk_moe_int4_w4a16_workspace_bytes", 64, 8, 48, 4096, 7168)
     # at least the align outputs plus one fp32 row per routed slot

@@ -1,0 +1,115 @@
+"""The INT4 grouped GEMM's per-slot rows against an error-bounded reference.
+
+The reference rounds every dequantised weight to bf16 before the contraction
+(w4a16.py:42-50: ``(nibble - 8) * scale`` in fp32, then ``.to(bf16)``). The
+spec's 2e-2 tolerance cannot tell rounded weights from exact ones, so these
+tests call the GEMM stage (``xk_moe_int4_w4a16_gemm``) directly and compare
+its fp32 row of every routed slot with a float64 contraction over the
+oracle's bf16-rounded weights, allowing only fp32 summation error:
+
+    |got - want| <= 2^-20 * sum_k |a_k * w_k| + 1e-30
+
+(K <= 7168 terms summed in fp32 add at most about K * 2^-24 relative to the
+absolute sum; the kernels sum in groups, which is far tighter). A kernel that
+contracted the exact (n - 8) * s products instead differs by the weights'
+rounding, about 2^-9 of each term, and fails the bound: the last test checks
+that the FAST mode (exact products) is told apart.
+"""
+from __future__ import annotations
+
+import pytest
+import torch
+
+from oracle.torch_ref import dequant_w4a16
+from tests._helpers import uniform_topk, zipf_topk
+from xkernels_amd import _lib, make_w4a16_weights
+
+pytestmark = pytest.mark.gpu
+
+REL = 2.0 ** -20
+
+
+def _gemm_rows(A, packed, scale, ids, flags=0):
+    """fp32 per-slot rows of the grouped GEMM (align with the library's block size)."""
+    M, K = A.shape
+    E, N, _ = packed.shape
+    top_k = ids.shape[1]
+    numel = M * top_k
+    dev = A.device
+    bs = _lib.query("xk_moe_int4_block_size", M, top_k, E)
+    max_pad = numel + (E + 1) * (bs - 1)
+    sorted_ids = torch.empty(max_pad, dtype=torch.int32, device=dev)
+    expert_ids = torch.empty((max_pad + bs - 1) // bs, dtype=torch.int32, device=dev)
+    num_post = torch.empty(1, dtype=torch.int32, device=dev)
+    offsets = torch.empty(E + 1, dtype=torch.int32, device=dev)
+    aws = torch.empty(max(1, _lib.query("xk_moe_align_workspace_bytes", numel, E)), dtype=torch.uint8,
+                      device=dev)
+    s = torch.cuda.current_stream().cuda_stream
+    _lib.call("xk_moe_align_block_size", ids.data_ptr(), numel, E, bs, None, 0, sorted_ids.data_ptr(),
+              expert_ids.data_ptr(), num_post.data_ptr(), offsets.data_ptr(), aws.data_ptr(),
+              aws.numel(), s)
+    parts = _lib.query("xk_moe_int4_gemm_parts", M, top_k, E, N, K, _lib.XK_DT_BF16, 32, flags)
+    out = torch.full((parts, numel, N), float("nan"), dtype=torch.float32, device=dev)
+    gws = torch.empty(max(256, _lib.query("xk_moe_int4_gemm_workspace_bytes", M, K)), dtype=torch.uint8,
+                      device=dev)
+    _lib.call("xk_moe_int4_w4a16_gemm", A.data_ptr(), _lib.XK_DT_BF16, M, K, packed.data_ptr(),
+              scale.data_ptr(), E, N, 32, ids.data_ptr(), top_k, None, 0, sorted_ids.data_ptr(),
+              offsets.data_ptr(), out.data_ptr(), flags, gws.data_ptr(), gws.numel(), s)
+    torch.cuda.synchronize()
+    return out.sum(0)
+
+
+def _bounded_check(A, packed, scale, ids, rows):
+    """Compares every routed slot's row, one expert at a time (float64 reference)."""
+    top_k = ids.shape[1]
+    flat = ids.reshape(-1).long()
+    worst = 0.0
+    for e in flat.unique().tolist():
+        slots = (flat == e).nonzero().reshape(-1)
+        W = dequant_w4a16(packed[e:e + 1], scale[e:e + 1], 32, out_dtype=torch.bfloat16)[0].double()
+        a = A[slots // top_k].double()
+        want = a @ W.T
+        bound = REL * (a.abs() @ W.abs().T) + 1e-30
+        err = (rows[slots].double() - want).abs()
+        ratio = float((err / bound).max())
+        worst = max(worst, ratio)
+        assert ratio <= 1.0, f"expert {e}: error {ratio:.3g} x the fp32-summation bound"
+    return worst
+
+
+def _device_inputs(M, E, N, K, ids, seed):
+    packed, scale, _ = make_w4a16_weights(E, N, K, 32, device="cuda", seed=seed, scale_hi=0.02)
+    g = torch.Generator(device="cuda").manual_seed(seed + 1)
+    A = torch.randn(M, K, generator=g, device="cuda").to(torch.bfloat16)
+    return A, packed, scale, ids.cuda()
+
+
+@pytest.mark.parametrize("M,E,N,K,top_k,routing", [
+    (64, 48, 4096, 7168, 8, "uniform"),    # C2, the headline (most experts one 16-row tile)
+    (16, 8, 1024, 2048, 2, "uniform"),     # C1
+    (64, 48, 7168, 2048, 8, "uniform"),    # the down projection of the same layer
+    (192, 16, 512, 1024, 4, "zipf"),       # experts with several 32-row passes
+    (40, 6, 160, 768, 3, "zipf"),          # K / 256 odd: one-tile passes only
+    (5, 4, 96, 512, 2, "uniform"),         # N not a multiple of 128
+    (1024, 8, 512, 1024, 4, "zipf"),       # prefill regime: the MFMA tile kernel
+])
+def test_rows_within_fp32_summation_error(M, E, N, K, top_k, routing):
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    ids = uniform_topk(M, top_k, E, 3) if routing == "uniform" else zipf_topk(M, top_k, E, 1.2, 3)
+    A, packed, scale, ids = _device_inputs(M, E, N, K, ids, 11)
+    rows = _gemm_rows(A, packed, scale, ids)
+    assert not torch.isnan(rows).any(), "a routed slot's row was not written"
+    _bounded_check(A, packed, scale, ids, rows)
+
+
+def test_fast_mode_is_told_apart():
+    """The exact-product (FAST) rows break the bound the RNE rows meet."""
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    M, E, N, K, top_k = 64, 48, 4096, 7168, 8
+    ids = uniform_topk(M, top_k, E, 3)
+    A, packed, scale, ids = _device_inputs(M, E, N, K, ids, 11)
+    rows = _gemm_rows(A, packed, scale, ids, flags=_lib.XK_INT4_FAST_DEQUANT)
+    with pytest.raises(AssertionError, match="fp32-summation bound"):
+        _bounded_check(A, packed, scale, ids, rows)

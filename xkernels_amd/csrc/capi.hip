@@ -37,7 +37,8 @@ int launch_topk_combine(const float* slot_out, int64_t M, int64_t top_k, int64_t
                         const float* topk_w, int mul_routed_weight, const int32_t* topk_ids,
                         int num_local, const int32_t* emap, int num_global, void* out,
                         int out_dtype, int nparts, hipStream_t stream);
-int int4_gemm_parts(int64_t E, int64_t N, int64_t K, int a_dtype, int group_size, int flags);
+int int4_gemm_parts(int64_t M, int64_t top_k, int64_t E, int64_t N, int64_t K, int a_dtype,
+                    int group_size, int flags);
 int int4_block_size();
 bool int4_use_stream(int a_dtype, int group_size, int64_t K);
 int64_t int4_gemm_workspace_bytes(int64_t M, int64_t K);
@@ -126,9 +127,9 @@ int32_t xk_moe_int4_block_size(int64_t M, int64_t top_k, int64_t E) {
   return int4_block_size();
 }
 
-int32_t xk_moe_int4_gemm_parts(int64_t E, int64_t N, int64_t K, int32_t a_dtype,
-                               int32_t group_size, int32_t flags) {
-  return int4_gemm_parts(E, N, K, a_dtype, group_size, flags);
+int32_t xk_moe_int4_gemm_parts(int64_t M, int64_t top_k, int64_t E, int64_t N, int64_t K,
+                               int32_t a_dtype, int32_t group_size, int32_t flags) {
+  return int4_gemm_parts(M, top_k, E, N, K, a_dtype, group_size, flags);
 }
 
 int64_t xk_moe_int4_w4a16_workspace_bytes(int64_t M, int64_t top_k, int64_t E, int64_t N,
@@ -136,7 +137,8 @@ int64_t xk_moe_int4_w4a16_workspace_bytes(int64_t M, int64_t top_k, int64_t E, i
   const int64_t numel = M * top_k;
   AlignScratch al(numel, int(E), int4_block_size());
   // sized for the largest number of partial planes any mode / dtype uses
-  const int64_t parts = int4_gemm_parts(E, N, K, XK_DT_BF16, 32, 0);
+  const int64_t parts = std::max(int4_gemm_parts(M, top_k, E, N, K, XK_DT_BF16, 32, 0),
+                                 int4_gemm_parts(M, top_k, E, N, K, XK_DT_FP32, 32, 0));
   return al.total + round_up(parts * numel * N * 4) + round_up(int4_gemm_workspace_bytes(M, K));
 }
 
@@ -189,7 +191,10 @@ int xk_moe_int4_w4a16(const void* A, int32_t a_dtype, int64_t M, int64_t K,
   const int64_t numel = M * top_k;
   AlignScratch al(numel, int(E), int4_block_size());
   float* slot_out = at<float>(workspace, al.total);
-  const int64_t gemm_ws = al.total + round_up(int4_gemm_parts(E, N, K, XK_DT_BF16, 32, 0) * numel * N * 4);
+  const int64_t parts = int4_gemm_parts(M, top_k, E, N, K, a_dtype, group_size, flags);
+  const int64_t gemm_ws = al.total + round_up(std::max(int4_gemm_parts(M, top_k, E, N, K, XK_DT_BF16, 32, 0),
+                                                       int4_gemm_parts(M, top_k, E, N, K, XK_DT_FP32, 32, 0)) *
+                                              numel * N * 4);
   const int32_t* sorted = nullptr;
   const int32_t* offsets = nullptr;
   if (int4_use_stream(a_dtype, group_size, K)) {
@@ -210,7 +215,7 @@ int xk_moe_int4_w4a16(const void* A, int32_t a_dtype, int64_t M, int64_t K,
     return rc;
   return launch_topk_combine(slot_out, M, top_k, N, topk_w, mul_routed_weight, topk_ids,
                              int(E), expert_map, num_global_experts, out, a_dtype,
-                             int4_gemm_parts(E, N, K, a_dtype, group_size, flags), stream);
+                             int(parts), stream);
 }
 
 int64_t xk_moe_mxfp4_workspace_bytes(int64_t M, int64_t top_k, int64_t E, int64_t hidden,

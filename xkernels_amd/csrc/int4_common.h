@@ -43,21 +43,22 @@ __device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t m, uint32_t k) {
 // Per-scale constants of dequant_rne (two VALU per scale, shared by every word
 // of the group).
 struct RneScale {
-  float s, m1032, s16, m72;  // s, -1032 s, s / 16, -72 s
+  float s, m1032, m72;  // s, -1032 s, -72 s
 };
 __device__ __forceinline__ RneScale rne_scale(float s) {
-  return RneScale{s, -1032.0f * s, 0.0625f * s, -72.0f * s};
+  return RneScale{s, -1032.0f * s, -72.0f * s};
 }
 
 // 8 nibbles of `w` (low nibble = lowest k) -> 8 bf16 = bf16_rne((n - 8) * s),
 // the reference's dequant rounding. Nibble pairs (d, d + 4) become two fp16
 // values with one v_and_or_b32 each: pairs 0 and 2 (nibbles at bits 0-3 of a
-// half word, mask `mlo` = 0x000F000F) read 1024 + n, pairs 1 and 3 (bits 4-7,
-// mask `mhi` = 0x00F000F0) read 1024 + 16 n, so one shift of the word serves
-// all four pairs. v_fma_mix_f32 then forms (1024 + n) s - 1032 s, resp.
-// (1024 + 16 n) (s / 16) - 72 s, both exactly (n - 8) s in fp32 (the terms fit
-// 24 bits; s / 16 is exact for any normal s >= 2^-122), and v_cvt_pk_bf16_f32
-// rounds to nearest even. Output element order: n0 n4 n1 n5 n2 n6 n3 n7.
+// half word, mask `mlo` = 0x000F000F, exponent bits 0x6400) read 1024 + n,
+// pairs 1 and 3 (bits 4-7, mask `mhi` = 0x00F000F0, exponent bits 0x5400)
+// read 64 + n, so one shift of the word serves all four pairs and every pair
+// uses the same multiplier. v_fma_mix_f32 then forms (1024 + n) s - 1032 s,
+// resp. (64 + n) s - 72 s, both exactly (n - 8) s in fp32 (every term fits 24
+// bits), and v_cvt_pk_bf16_f32 rounds to nearest even. Output element order:
+// n0 n4 n1 n5 n2 n6 n3 n7.
 __device__ __forceinline__ bf16x8 dequant_rne(uint32_t w, const RneScale& k, uint32_t mlo,
                                               uint32_t mhi) {
   typedef _Float16 h2 __attribute__((ext_vector_type(2)));
@@ -65,14 +66,14 @@ __device__ __forceinline__ bf16x8 dequant_rne(uint32_t w, const RneScale& k, uin
   typedef __bf16 b2 __attribute__((ext_vector_type(2)));
   const uint32_t w8 = w >> 8;
   const h2 x[4] = {__builtin_bit_cast(h2, and_or(w, mlo, 0x64006400u)),
-                   __builtin_bit_cast(h2, and_or(w, mhi, 0x64006400u)),
+                   __builtin_bit_cast(h2, and_or(w, mhi, 0x54005400u)),
                    __builtin_bit_cast(h2, and_or(w8, mlo, 0x64006400u)),
-                   __builtin_bit_cast(h2, and_or(w8, mhi, 0x64006400u))};
+                   __builtin_bit_cast(h2, and_or(w8, mhi, 0x54005400u))};
   u32x4 b;
 #pragma unroll
   for (int d = 0; d < 4; ++d) {
-    const float m = (d & 1) ? k.s16 : k.s, c = (d & 1) ? k.m72 : k.m1032;
-    const f2 v = {fmaf(static_cast<float>(x[d][0]), m, c), fmaf(static_cast<float>(x[d][1]), m, c)};
+    const float c = (d & 1) ? k.m72 : k.m1032;
+    const f2 v = {fmaf(static_cast<float>(x[d][0]), k.s, c), fmaf(static_cast<float>(x[d][1]), k.s, c)};
     b[d] = __builtin_bit_cast(uint32_t, __builtin_convertvector(v, b2));
   }
   return __builtin_bit_cast(bf16x8, b);

@@ -779,23 +779,21 @@ bool int4_use_stream(int a_dtype, int group_size, int64_t K) {
   return a_dtype == XK_DT_BF16 && group_size == 32 && K % 32 == 0 && K >= 32;
 }
 
-// Number of fp32 partial planes the grouped GEMM writes (every kernel here
-// contracts the full K range per output, so one).
-int int4_gemm_parts(int64_t E, int64_t N, int64_t K, int a_dtype, int group_size, int flags) {
-  (void)E; (void)N; (void)K; (void)a_dtype; (void)group_size; (void)flags;
-  return 1;
-}
-
 bool int4_prefill_ok(int a_dtype, int group_size, int64_t K, int64_t N, int64_t E);
 bool int4_ksplit_ok(int64_t K, int64_t N, int64_t E, int64_t numel);
-
+bool int4_rs_ok(int64_t M, int64_t K, int64_t N, int64_t E);
+int rs_slices(int64_t K);
+int launch_int4_rs(const void* A, int64_t M, int64_t K, const int32_t* packed,
+                   const uint16_t* scale, int64_t E, int64_t N, int64_t numel, int64_t top_k,
+                   const int32_t* sorted_ids, const int32_t* offsets, float* slot_out,
+                   hipStream_t stream);
 int launch_int4_prefill(const void* A, int64_t K, const int32_t* packed, const uint16_t* scale,
                         int64_t E, int64_t N, int64_t numel, int64_t top_k,
                         const int32_t* sorted_ids, const int32_t* offsets, float* slot_out,
                         hipStream_t stream);
 
 // Routed rows per expert (on average) from which the tile kernel replaces the
-// weight-streaming kernel.
+// weight-streaming kernels.
 constexpr int64_t kPrefillRowsPerExpert = 64;
 
 // FAST-mode activation preparation (int4_decode.hip): scratch layout and launch.
@@ -807,6 +805,37 @@ int launch_int4_ksplit(const Int4Prep& prep, int64_t K, const int32_t* packed,
                        const uint16_t* scale, int64_t E, int64_t N, int64_t numel, int64_t top_k,
                        const int32_t* sorted_ids, const int32_t* offsets, float* slot_out,
                        hipStream_t stream);
+
+// The grouped-GEMM kernel a call runs, from its shapes and flags only (not
+// from pointers), so that the number of partial planes is known before the
+// call. Pointer alignment the chosen kernel needs is checked at launch.
+enum class Int4Kernel { kSimple, kStreamV1, kStreamV2, kKsplit, kRs, kTile };
+
+Int4Kernel int4_choose(int64_t M, int64_t top_k, int64_t E, int64_t N, int64_t K, int a_dtype,
+                       int group_size, int flags) {
+  if (!int4_use_stream(a_dtype, group_size, K)) return Int4Kernel::kSimple;
+  const int64_t numel = M * top_k;
+  const bool tile_ok = int4_prefill_ok(a_dtype, group_size, K, N, E);
+  const bool want_tile = (flags & XK_INT4_FORCE_TILE) ||
+                         (numel >= kPrefillRowsPerExpert * E && !(flags & XK_INT4_FORCE_STREAM));
+  if (tile_ok && want_tile && !(flags & XK_INT4_V1)) return Int4Kernel::kTile;
+  if (K % 256 != 0 || (K / 32) % 8 != 0 || (flags & XK_INT4_V1)) return Int4Kernel::kStreamV1;
+  if (flags & XK_INT4_FAST_DEQUANT)
+    return (numel <= 16 * E && int4_ksplit_ok(K, N, E, numel) && !(flags & XK_INT4_V2))
+               ? Int4Kernel::kKsplit
+               : Int4Kernel::kStreamV2;
+  if (!(flags & XK_INT4_V2) && int4_rs_ok(M, K, N, E)) return Int4Kernel::kRs;
+  return Int4Kernel::kStreamV2;
+}
+
+// Number of fp32 partial planes [parts, M * top_k, N] the grouped GEMM
+// writes: the K slices of the decode stream kernel, else one.
+int int4_gemm_parts(int64_t M, int64_t top_k, int64_t E, int64_t N, int64_t K, int a_dtype,
+                    int group_size, int flags) {
+  return int4_choose(M, top_k, E, N, K, a_dtype, group_size, flags) == Int4Kernel::kRs
+             ? rs_slices(K)
+             : 1;
+}
 
 int launch_int4_gemm(const void* A, int a_dtype, int64_t M, int64_t K, const int32_t* packed,
                      const uint16_t* scale, int64_t E, int64_t N, int group_size,
@@ -823,20 +852,27 @@ int launch_int4_gemm(const void* A, int a_dtype, int64_t M, int64_t K, const int
   const int64_t numel = M * top_k;
   XK_REQUIRE(numel < (int64_t(1) << 30), "int4: M*top_k too large");
   if (numel == 0) return XK_OK;
-  if (int4_use_stream(a_dtype, group_size, K)) {
-    XK_REQUIRE(sorted_ids && offsets, "int4: stream kernel needs align outputs");
+  const Int4Kernel kern = int4_choose(M, top_k, E, N, K, a_dtype, group_size, flags);
+  if (kern != Int4Kernel::kSimple) {
+    XK_REQUIRE(sorted_ids && offsets, "int4: stream kernels need align outputs");
     XK_REQUIRE(reinterpret_cast<uintptr_t>(A) % 16 == 0, "int4: A must be 16-byte aligned");
-    const bool tile_ok = int4_prefill_ok(a_dtype, group_size, K, N, E) &&
-                         reinterpret_cast<uintptr_t>(packed) % 16 == 0;
-    const bool want_tile = (flags & XK_INT4_FORCE_TILE) ||
-                           (numel >= kPrefillRowsPerExpert * E && !(flags & XK_INT4_FORCE_STREAM));
-    if (tile_ok && want_tile && !(flags & XK_INT4_V1))
+  }
+  if (kern == Int4Kernel::kTile || kern == Int4Kernel::kRs || kern == Int4Kernel::kKsplit ||
+      kern == Int4Kernel::kStreamV2)
+    XK_REQUIRE(reinterpret_cast<uintptr_t>(packed) % 16 == 0 &&
+                   reinterpret_cast<uintptr_t>(scale) % 16 == 0,
+               "int4: packed weights and scales must be 16-byte aligned");
+  switch (kern) {
+    case Int4Kernel::kTile:
       return launch_int4_prefill(A, K, packed, scale, E, N, numel, top_k, sorted_ids, offsets,
                                  slot_out, stream);
-    StreamArgs a{static_cast<const uint16_t*>(A), reinterpret_cast<const uint32_t*>(packed),
-                 scale, sorted_ids, offsets, slot_out, int(K), int(N), int(numel), int(top_k),
-                 int((K / 32) % 8 == 0 && reinterpret_cast<uintptr_t>(scale) % 16 == 0)};
-    if (K % 256 == 0 && a.scale_vec && !(flags & XK_INT4_V1)) {
+    case Int4Kernel::kRs:
+      return launch_int4_rs(A, M, K, packed, scale, E, N, numel, top_k, sorted_ids, offsets,
+                            slot_out, stream);
+    case Int4Kernel::kKsplit:
+    case Int4Kernel::kStreamV2: {
+      StreamArgs a{static_cast<const uint16_t*>(A), reinterpret_cast<const uint32_t*>(packed),
+                   scale, sorted_ids, offsets, slot_out, int(K), int(N), int(numel), int(top_k), 1};
       V2Args v2{a, int(E), nullptr};
       constexpr int kW = XK_INT4_STREAM_WAVES;
       const int64_t items = E * cdiv(N, kW * kColsPerWave);
@@ -857,7 +893,7 @@ int launch_int4_gemm(const void* A, int a_dtype, int64_t M, int64_t K, const int
         if (int rc = launch_int4_prep(static_cast<const uint16_t*>(A), M, K, prep, stream)) return rc;
         v2.s.A = prep.a16;
         v2.a_exp = prep.a_exp;
-        if (one_tile && int4_ksplit_ok(K, N, E, numel) && !(flags & XK_INT4_V2))
+        if (kern == Int4Kernel::kKsplit)
           return launch_int4_ksplit(prep, K, packed, scale, E, N, numel, top_k, sorted_ids,
                                     offsets, slot_out, stream);
         if (one_tile)
@@ -873,15 +909,22 @@ int launch_int4_gemm(const void* A, int a_dtype, int64_t M, int64_t K, const int
       XK_CHECK_LAUNCH("int4_stream_v2");
       return XK_OK;
     }
-    const dim3 grid(static_cast<unsigned>(cdiv(N, kColsPerWG)), static_cast<unsigned>(E));
-    if (flags & XK_INT4_FAST_DEQUANT) {
-      hipLaunchKernelGGL(int4_stream_gemm, grid, dim3(256), 0, stream, a);
-      XK_CHECK_LAUNCH("int4_stream_gemm");
-    } else {
-      hipLaunchKernelGGL(int4_stream_gemm_rne, grid, dim3(256), 0, stream, a);
-      XK_CHECK_LAUNCH("int4_stream_gemm_rne");
+    case Int4Kernel::kStreamV1: {
+      StreamArgs a{static_cast<const uint16_t*>(A), reinterpret_cast<const uint32_t*>(packed),
+                   scale, sorted_ids, offsets, slot_out, int(K), int(N), int(numel), int(top_k),
+                   int((K / 32) % 8 == 0 && reinterpret_cast<uintptr_t>(scale) % 16 == 0)};
+      const dim3 grid(static_cast<unsigned>(cdiv(N, kColsPerWG)), static_cast<unsigned>(E));
+      if (flags & XK_INT4_FAST_DEQUANT) {
+        hipLaunchKernelGGL(int4_stream_gemm, grid, dim3(256), 0, stream, a);
+        XK_CHECK_LAUNCH("int4_stream_gemm");
+      } else {
+        hipLaunchKernelGGL(int4_stream_gemm_rne, grid, dim3(256), 0, stream, a);
+        XK_CHECK_LAUNCH("int4_stream_gemm_rne");
+      }
+      return XK_OK;
     }
-    return XK_OK;
+    case Int4Kernel::kSimple:
+      break;
   }
   const int64_t total = numel * N;
   const dim3 grid(static_cast<unsigned>(cdiv(total, 256)));

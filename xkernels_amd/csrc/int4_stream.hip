@@ -1,0 +1,363 @@
+// INT4 W4A16 decode-regime grouped GEMM for gfx950 with the reference's
+// bf16-rounded weights: the _fused_moe_int4_kernel of
+// src/xkernels/ops/moe/triton/moe_int4_kernel.py:78-272, math of the oracle
+// reference.py:22-70 with the dequant of w4a16.py:21-50
+// (W = bf16((nibble - 8) * scale), then an fp32-accumulated contraction).
+//
+// Decode experts hold ~11 routed rows, so every packed weight byte feeds one
+// 16-row MFMA tile and the kernel is a weight stream (792 MB at the headline
+// shape) with ~2.1 VALU instructions of exact dequant per weight. Measured on
+// MI355X, VALU work and the HBM stream of a CU do not overlap (their times
+// add, even when they run in different waves), so the design removes every
+// other cost from the stream and keeps the dequant at its minimum:
+//   * work item = (expert, 16-row pass, K slice, 32 output columns). K is cut
+//     into S slices only as far as one slice of the pass's activations fits
+//     the LDS (S = 2 at K = 7168); every slice writes its own fp32 partial
+//     plane (plain stores, summed by the combine in a fixed order), so no
+//     workgroup ever switches slices inside a segment;
+//   * the items of all experts are split evenly over one 8-wave workgroup per
+//     CU (every CU streams the same number of weight bytes); a workgroup's
+//     contiguous range holds one or two (expert, pass, slice) segments;
+//   * the segment's activations (16 rows x K / S bf16, 112 KiB) are loaded
+//     once into LDS by direct-to-LDS loads, already in MFMA operand order (a
+//     1 KiB operand is one ds_read_b128 at lane * 16, conflict-free), then
+//     each lane reorders its own 8 values like the nibble unpack;
+//   * each wave streams its column pairs with no barrier: a ring of lines
+//     (4 x 16-byte weight loads and 2 x 16-byte scale loads per 128-byte line
+//     of 32 columns) in flight, one line dequantised and contracted per step;
+//   * lane (c, q) of a load reads bytes 64 h + 16 q of column c's line: the
+//     whole quantisation group 4 h + q, one contiguous 64-byte half line per
+//     column and instruction. Word j of it feeds MFMA j, so an MFMA contracts
+//     four groups (one per lane group) and each lane applies its own group's
+//     scale during the dequant;
+//   * dequant: dequant_rne (int4_common.h), bit-identical to the reference's
+//     bf16((n - 8) * s).
+#include "int4_common.h"
+
+#ifndef XK_RS_VARIANT
+#define XK_RS_VARIANT 0  // diagnostic builds only: 2 no MFMA, 3 loads only
+#endif
+
+namespace xk {
+
+int device_cu_count();
+
+namespace {
+
+constexpr int kRsWaves = 8;                 // waves per workgroup (one workgroup per CU)
+constexpr int kRsThreads = kRsWaves * 64;
+constexpr int kRsMaxCp = 3;                 // column pairs per wave per chunk
+constexpr int kRsRing = 2;                  // ring slots: line k + 1 in flight while line k computes
+constexpr int kRsLdsA = 112 * 1024;         // bytes of LDS for one activation slice
+constexpr int kRsMaxE = 256;
+
+struct RsArgs {
+  const uint16_t* A;        // [M, K] bf16
+  const uint32_t* packed;   // [E, N, K/8]
+  const uint16_t* scale;    // [E, N, K/32] bf16
+  const int32_t* sorted_ids;
+  const int32_t* offsets;   // [E+1] padded prefix in slots (multiples of 16)
+  float* out;               // [S, numel, N] partial planes
+  int K, N, E, numel, top_k;
+  int slices;               // S: K slices (16 rows x K / S bf16 fit kRsLdsA)
+  uint32_t a_bytes;         // bytes of A (buffer resource range)
+};
+
+// s_waitcnt vmcnt(n) as a real instruction the compiler accounts for (gfx9
+// encoding: vmcnt bits 3:0 and 15:14, expcnt and lgkmcnt left at their maxima).
+#define XK_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (((n) >> 4) << 14) | 0x0F70)
+
+// Workgroup barrier that waits for this wave's LDS operations only; the
+// weight loads in flight stay in flight.
+__device__ __forceinline__ void lds_sync() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+template <typename T> __device__ __forceinline__ T uniform(T x) {
+  return __builtin_amdgcn_readfirstlane(x);
+}
+
+// Buffer descriptor (gfx9 layout: base, num_records, raw 32-bit access) held
+// in SGPRs.
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ i32x4 make_rsrc(const void* base, uint32_t bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  return i32x4{static_cast<int32_t>(uniform(static_cast<uint32_t>(a))),
+               static_cast<int32_t>(uniform(static_cast<uint32_t>(a >> 32))),
+               static_cast<int32_t>(uniform(bytes)), 0x00020000};
+}
+
+// Direct-to-LDS 16-byte buffer load: lane i's 16 bytes from voff + soff land
+// at lds + 16 i. Issued as inline assembly so that the compiler does not make
+// unrelated LDS reads wait for it; the kernel waits for these loads itself
+// (XK_WAIT_VMCNT) before it reads the buffer.
+__device__ __forceinline__ void dma_16(i32x4 rsrc, const void* lds, int voff, int soff) {
+  const uint32_t m0 = uniform(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds)));
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+               :
+               : "s"(m0), "v"(voff), "s"(rsrc), "s"(uniform(soff))
+               : "memory", "m0");
+}
+
+// f(integral_constant<int, I>) for I = 0 .. N-1: indices that are constants
+// before optimisation, so register arrays indexed by them stay in registers.
+template <int N, typename F, int I = 0> __device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    static_for<N, F, I + 1>(static_cast<F&&>(f));
+  }
+}
+
+__global__ void __launch_bounds__(kRsThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+int4_stream_rne(RsArgs p) {
+  __shared__ __attribute__((aligned(16))) u32x4 a_lds[kRsLdsA / 16];
+  __shared__ int pref[kRsMaxE + 1];
+  __shared__ int row_slot[16];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = uniform(tid >> 6);
+  const int c16 = lane & 15, q = lane >> 4;
+  const int K = p.K, N = p.N, E = p.E, G = K >> 5, KW = K >> 3;
+  const int S = p.slices, Ks = K / S, nl = Ks >> 8;
+  const int ncp = N >> 5;            // column pairs per expert
+  const int nblk = nl * 8;           // 1 KiB operand blocks of one activation slice
+  const uint32_t kNibMask = in_vgpr(0x000F000Fu), kNibMaskHi = in_vgpr(0x00F000F0u);
+
+  // Items per expert: 16-row passes x slices x column pairs. Prefix by wave
+  // 0 into LDS.
+  if (wave == 0) {
+    int run = 0;
+    for (int base = 0; base < E; base += 64) {
+      const int e = base + lane;
+      int x = e < E ? ((p.offsets[e + 1] - p.offsets[e]) >> 4) * S * ncp : 0;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int y = __shfl_up(x, o);
+        if (lane >= o) x += y;
+      }
+      if (e < E) pref[e + 1] = run + x;
+      run += __shfl(x, 63);
+    }
+    if (lane == 0) pref[0] = 0;
+  }
+  __syncthreads();
+  const int total_items = uniform(pref[E]);
+  const int gsz = gridDim.x, b = blockIdx.x;
+  const int item_beg = static_cast<int>(static_cast<int64_t>(total_items) * b / gsz);
+  const int item_end = static_cast<int>(static_cast<int64_t>(total_items) * (b + 1) / gsz);
+
+  const int w_lane = c16 * KW * 4 + q * 16;  // bytes; + 64 h: group 4 h + q of the line
+  const int s_lane = c16 * G * 2;            // bytes: the line's 8 group scales
+  // v_perm_b32 selector: bytes 2q, 2q+1 of a scale word pair -> bits 16-31
+  const uint32_t s_sel = ((2u * q + 1) << 24) | ((2u * q) << 16) | 0x0C0Cu;
+  const i32x4 ra = make_rsrc(p.A, p.a_bytes);
+  const int64_t plane = static_cast<int64_t>(p.numel) * N;
+
+  // Activation slice of a segment -> LDS, in operand order: 1 KiB block
+  // blk = (line * 2 + h) * 4 + j holds, at lane qq * 16 + r, the 8 values
+  // k = s Ks + line * 256 + (4 h + qq) * 32 + 8 j .. + 7 of row r, reordered
+  // like the nibble unpack. Rows of pad slots read token 0 (never stored).
+  auto load_segment = [&](int row0, int s) __attribute__((always_inline)) {
+    lds_sync();  // every wave is done with the previous segment
+    if (tid < 16) {
+      const int sid = p.sorted_ids[row0 + tid];
+      row_slot[tid] = sid < p.numel ? sid : -1;
+    }
+    const int sid = p.sorted_ids[row0 + c16];
+    const int a_voff = (sid < p.numel ? sid / p.top_k : 0) * K * 2 + q * 64;
+    for (int blk = wave; blk < nblk; blk += kRsWaves) {
+      const int j = blk & 3, h = (blk >> 2) & 1, line = blk >> 3;
+      dma_16(ra, &a_lds[blk * 64], a_voff, (s * Ks + line * 256 + 128 * h + 8 * j) * 2);
+    }
+    XK_WAIT_VMCNT(0);
+    for (int blk = wave; blk < nblk; blk += kRsWaves) {
+      u32x4& x = a_lds[blk * 64 + lane];
+      const u32x4 v = x;
+      uint32_t in[4] = {v[0], v[1], v[2], v[3]}, o[4];
+      perm8(in, o);
+      x = u32x4{o[0], o[1], o[2], o[3]};
+    }
+    lds_sync();
+  };
+
+  // One chunk: this wave's `cnt` column pairs from `my_lo` of expert e,
+  // slice s, each nl lines; results to plane s.
+  auto run_chunk = [&](int e, int s, int my_lo, int cnt) __attribute__((always_inline)) {
+    if (cnt == 0) return;
+    const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint32_t*>(p.packed + static_cast<int64_t>(e) * N * KW), 0, N * KW * 4, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(p.scale + static_cast<int64_t>(e) * N * G), 0, N * G * 2, 0x00020000);
+    // Steps (lines) of the chunk, padded to a multiple of kRsRing with dummy
+    // steps that re-load the last line and compute nothing, so that the
+    // steady-state loop issues every load unconditionally.
+    const int steps = cnt * nl;
+    const int padded = (steps + kRsRing - 1) / kRsRing * kRsRing;
+    int pst = 0, pi = 0, pl = 0;  // prefetch cursor: step, pair, line
+    int cst = 0, ci = 0, cl = 0;  // compute cursor
+
+    struct Slot {
+      u32x4 w[2][2];  // weights: [column tile][group 4 h + q]
+      u32x4 s[2];     // the line's 8 group scales: [column tile]
+    };
+    Slot rg[kRsRing];
+    auto issue = [&](Slot& sl) __attribute__((always_inline)) {
+      const int cp = my_lo + pi;
+      const int wo = cp * 32 * KW * 4 + s * (Ks >> 1) + pl * 128;
+      const int so = cp * 32 * G * 2 + (s * (Ks >> 5) + pl * 8) * 2;
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+          sl.w[c][h] = __builtin_amdgcn_raw_buffer_load_b128(rw, w_lane + 64 * h, wo + c * 16 * KW * 4, 0);
+        sl.s[c] = __builtin_amdgcn_raw_buffer_load_b128(rs, s_lane, so + c * 16 * G * 2, 0);
+      }
+      // advance (value selects keep the cursor in scalar registers)
+      const int np = pst + 1;
+      const int pl1 = pl + (np < steps ? 1 : 0);
+      const bool lwrap = pl1 == nl;
+      pst = np;
+      pi += lwrap ? 1 : 0;
+      pl = lwrap ? 0 : pl1;
+    };
+
+    f32x4 acc[2];  // the current column pair's two 16 x 16 tiles
+    acc[0] = acc[1] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    auto compute = [&](const Slot& sl) __attribute__((always_inline)) {
+      const int lbase = cl * (8 * 64) + lane;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        RneScale ks[2];
+#pragma unroll
+        for (int c = 0; c < 2; ++c)  // bf16 scale of group 4 h + q -> fp32 (one v_perm_b32)
+          ks[c] = rne_scale(__uint_as_float(__builtin_amdgcn_perm(sl.s[c][2 * h + 1], sl.s[c][2 * h], s_sel)));
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          bf16x8 bfrag[2];
+#pragma unroll
+          for (int c = 0; c < 2; ++c) {
+#if XK_RS_VARIANT == 3
+            bfrag[c] = __builtin_bit_cast(bf16x8, sl.w[c][h]);
+#else
+            bfrag[c] = dequant_rne(sl.w[c][h][j], ks[c], kNibMask, kNibMaskHi);
+#endif
+          }
+#if XK_RS_VARIANT == 2 || XK_RS_VARIANT == 3
+#pragma unroll
+          for (int c = 0; c < 2; ++c) {
+            const u32x4 x = __builtin_bit_cast(u32x4, bfrag[c]);
+            acc[c][j] = __uint_as_float(__float_as_uint(acc[c][j]) ^ x[0] ^ x[1] ^ x[2] ^ x[3]);
+          }
+#else
+          const bf16x8 afrag = __builtin_bit_cast(bf16x8, a_lds[lbase + (h * 4 + j) * 64]);
+#pragma unroll
+          for (int c = 0; c < 2; ++c)
+            acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(afrag, bfrag[c], acc[c], 0, 0, 0);
+#endif
+        }
+      }
+    };
+
+    // End of a column pair: its partial rows (this slice) to plane s.
+    auto flush = [&](int i) __attribute__((always_inline)) {
+      float* base = p.out + s * plane + (my_lo + i) * 32 + c16;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int slot = row_slot[4 * q + r];
+        if (slot >= 0) {
+          base[static_cast<int64_t>(slot) * N] = acc[0][r];
+          base[static_cast<int64_t>(slot) * N + 16] = acc[1][r];
+        }
+      }
+      acc[0] = acc[1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    };
+
+    // Ring of kRsRing slots: step k issues the loads of step k + kRsRing - 1
+    // into the slot freed by step k - 1, then computes step k.
+    static_for<kRsRing - 1>([&](auto d) {
+      issue(rg[d]);
+      __builtin_amdgcn_sched_barrier(0);
+    });
+    auto step = [&](auto slot) __attribute__((always_inline)) {
+      constexpr int nxt = (decltype(slot)::value + kRsRing - 1) % kRsRing;
+      issue(rg[nxt]);
+      __builtin_amdgcn_sched_barrier(0);
+      const bool real = cst < steps;
+      if (real) compute(rg[slot]);
+      const int cl1 = cl + (real ? 1 : 0);
+      const bool tend = cl1 == nl;
+      if (tend) flush(ci);
+      __builtin_amdgcn_sched_barrier(0);
+      cl = tend ? 0 : cl1;
+      ci += tend ? 1 : 0;
+      ++cst;
+    };
+    for (int st = 0; st < padded; st += kRsRing)
+      static_for<kRsRing>([&](auto d) { step(d); });
+    // The ring's loads past the last step must land before their registers
+    // are reused.
+    XK_WAIT_VMCNT(0);
+  };
+
+  // Walk this workgroup's item range: segments of one (expert, pass, slice),
+  // cut into chunks of at most kRsWaves * kRsMaxCp column pairs.
+  int loaded = -1;  // first item of the segment whose activations are in LDS
+  int pos = item_beg;
+  while (pos < item_end) {
+    int lo = 0, hi = E;  // largest e with pref[e] <= pos
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (pref[mid] <= pos) lo = mid; else hi = mid;
+    }
+    const int e = uniform(lo);
+    const int local = pos - pref[e];
+    const int seg = local / ncp, cp0 = local - seg * ncp;  // seg = pass * S + slice
+    const int pass = seg / S, s = seg - pass * S;
+    const int cpe = min(ncp, cp0 + (item_end - pos));
+    const int seg_id = uniform(pos - cp0);
+    if (seg_id != loaded) {
+      load_segment(uniform(p.offsets[e] + pass * 16), s);
+      loaded = seg_id;
+    }
+    for (int c0 = cp0; c0 < cpe; c0 += kRsWaves * kRsMaxCp) {
+      const int lc = min(kRsWaves * kRsMaxCp, cpe - c0);
+      const int my_lo = c0 + wave * lc / kRsWaves;
+      const int cnt = c0 + (wave + 1) * lc / kRsWaves - my_lo;
+      run_chunk(e, s, my_lo, cnt);
+    }
+    pos += cpe - cp0;
+  }
+}
+
+}  // namespace
+
+// K slices for one 16-row pass: the fewest (K / 256 split evenly) whose
+// activation block fits the LDS buffer.
+int rs_slices(int64_t K) {
+  if (K % 256 != 0) return 0;
+  const int64_t lines = K / 256;
+  for (int64_t s = 1; s <= lines; ++s)
+    if (lines % s == 0 && 16 * (K / s) * 2 <= kRsLdsA) return static_cast<int>(s);
+  return 0;
+}
+
+bool int4_rs_ok(int64_t M, int64_t K, int64_t N, int64_t E) {
+  return K % 256 == 0 && N % 32 == 0 && E <= kRsMaxE && rs_slices(K) > 0 &&
+         N * (K / 8) * 4 < (int64_t(1) << 31) && M * K * 2 < (int64_t(1) << 31);
+}
+
+int launch_int4_rs(const void* A, int64_t M, int64_t K, const int32_t* packed,
+                   const uint16_t* scale, int64_t E, int64_t N, int64_t numel, int64_t top_k,
+                   const int32_t* sorted_ids, const int32_t* offsets, float* slot_out,
+                   hipStream_t stream) {
+  RsArgs a{static_cast<const uint16_t*>(A), reinterpret_cast<const uint32_t*>(packed), scale,
+           sorted_ids, offsets, slot_out, int(K), int(N), int(E), int(numel), int(top_k),
+           rs_slices(K), static_cast<uint32_t>(M * K * 2)};
+  hipLaunchKernelGGL(int4_stream_rne, dim3(static_cast<unsigned>(device_cu_count())),
+                     dim3(kRsThreads), 0, stream, a);
+  XK_CHECK_LAUNCH("int4_stream_rne");
+  return XK_OK;
+}
+
+}  // namespace xk
