@@ -221,12 +221,25 @@ def moe_mxfp4_ref(A, w13, w13_scale, w2, w2_scale, topk_ids, topk_w, b13=None, b
 
 # ------------------------------------------------------------ registration ----
 
+# The Op Specs name the reference repository's own oracle functions.
+SPEC_REFERENCES = {
+    "xkernels.ops.moe.reference:moe_w4a16_ref": moe_w4a16_ref,
+    "xkernels.ops.moe.w4a16:moe_align_block_size_ref": moe_align_block_size_ref,
+    "xkernels.ops.moe.sum_reduce:moe_sum_reduce_ref": moe_sum_reduce_ref,
+    "xkernels.ops.moe.mxfp4_reference:moe_mxfp4_ref": moe_mxfp4_ref,
+}
+
+
 def register_reference_backends() -> None:
-    """Install the oracle as the REFERENCE backend of the four kernels (test harness)."""
+    """Install the oracle as the REFERENCE backend of the four kernels and as the
+    resolution of the Op Specs' reference paths (test harness only)."""
     from xkernels_amd._backends import Backend
     from xkernels_amd._dispatch import register
+    from xkernels_amd.registry import bind_reference
 
     register("moe_int4_w4a16", Backend.REFERENCE)(moe_w4a16_ref)
     register("moe_align_block_size", Backend.REFERENCE)(moe_align_block_size_ref)
     register("moe_sum_reduce", Backend.REFERENCE)(moe_sum_reduce_ref)
     register("moe_mxfp4", Backend.REFERENCE)(moe_mxfp4_ref)
+    for path, fn in SPEC_REFERENCES.items():
+        bind_reference(path, fn)

@@ -25,9 +25,7 @@ OPS = ["moe_int4_w4a16@1.0.0", "moe_align_block_size@1.0.0", "moe_sum_reduce@1.0
 def fake_kernel():
     name = "test_fake_kernel"
     yield name
-    for b in list(_dispatch.registered_backends(name)):
-        _dispatch.unregister(name, b)
-    _dispatch._BACKEND_FAILURES.pop(name, None)
+    _dispatch.forget(name)
 
 
 def test_dispatch_explicit_env_and_auto(fake_kernel, monkeypatch):
@@ -83,7 +81,8 @@ def test_reference_fallback_warns_on_gpu_tensors(fake_kernel, monkeypatch):
 def test_package_registers_hip_for_every_op():
     for k in ("moe_int4_w4a16", "moe_align_block_size", "moe_sum_reduce", "moe_mxfp4"):
         assert Backend.HIP in _dispatch.registered_backends(k)
-    assert not any(f for f in _dispatch.backend_failures().values()), _dispatch.backend_diagnostics()
+    diag = _dispatch.backend_diagnostics()
+    assert not any(v["failures"] for v in diag.values()), diag
 
 
 def test_hip_ops_refuse_cpu_tensors():
@@ -150,10 +149,25 @@ def test_specs_cards_and_sweeps_load():
         backends = {c.backend.name for c in cards[op].values()}
         assert {"HIP", "REFERENCE"} <= backends
         hip = next(c for c in cards[op].values() if c.backend.name == "HIP")
-        assert hip.arch.family == "amd_cdna4"
+        assert hip.arch_family == "amd_cdna4"
         assert len(load_shape_sweep(specs[op].shape_sweep)) >= 1
         assert input_gen.has_generator(op) and cost_model.has_model(op)
     assert get_card("moe_int4_w4a16.hip@1.0.0").implements == "moe_int4_w4a16@1.0.0"
+
+
+def test_specs_keep_the_reference_numerics():
+    """The three Op Specs the reference defines keep its numerics block (the
+    reference callable path included); the harness resolves the path through
+    bind_reference in this checkout."""
+    from xkernels_amd.registry import reference_callable
+
+    want = {"moe_int4_w4a16@1.0.0": "xkernels.ops.moe.reference:moe_w4a16_ref",
+            "moe_align_block_size@1.0.0": "xkernels.ops.moe.w4a16:moe_align_block_size_ref",
+            "moe_sum_reduce@1.0.0": "xkernels.ops.moe.sum_reduce:moe_sum_reduce_ref",
+            "moe_mxfp4@1.0.0": "xkernels.ops.moe.mxfp4_reference:moe_mxfp4_ref"}
+    for op, path in want.items():
+        assert all_specs()[op].reference == path
+        assert callable(reference_callable(op))
 
 
 def test_constraints():

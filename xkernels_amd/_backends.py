@@ -1,8 +1,8 @@
-"""Backend identifiers and vendor detection.
+"""Backend identifiers and the vendor of the running torch build.
 
-Same names and values as the reference's ``xkernels._backends``
-(src/xkernels/_backends.py:9-27) so Impl Cards and ``XKERNELS_BACKEND`` values
-carry over unchanged.
+The ``Backend`` names and values are the reference's plugin vocabulary
+(src/xkernels/_backends.py:9-18): Impl Cards and ``XKERNELS_BACKEND`` use
+them, so they are kept as they are.
 """
 from __future__ import annotations
 
@@ -19,14 +19,9 @@ class Backend(enum.Enum):
 
 
 def detect_vendor() -> str:
-    """'amd' on a ROCm build of torch, 'nvidia' on a CUDA build with a GPU, else 'none'."""
-    if getattr(torch.version, "hip", None):
+    """Which preference list the dispatcher uses: a ROCm build of torch is
+    'amd' (HIP first) whether or not a device is visible, a CUDA build with a
+    device is 'nvidia', anything else 'none' (CPU only)."""
+    if torch.version.hip:
         return "amd"
-    if getattr(torch.version, "cuda", None) and torch.cuda.is_available():
-        return "nvidia"
-    return "none"
-
-
-def device_of(tensor: torch.Tensor) -> str:
-    """'cpu' or 'cuda' (ROCm devices report 'cuda')."""
-    return tensor.device.type
+    return "nvidia" if (torch.version.cuda and torch.cuda.is_available()) else "none"

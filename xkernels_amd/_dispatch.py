@@ -1,205 +1,206 @@
-"""Backend registry and selection — the plugin boundary of the MoE ops.
+"""Backend selection for the MoE ops — the plugin boundary the public op wrappers
+call.
 
-Mirrors the reference's ``xkernels._dispatch`` contract
-(src/xkernels/_dispatch.py:19-247): backends self-register with
-``@register(kernel, Backend.X)``; ``dispatch(kernel, *args, backend="auto",
-**kw)`` resolves explicit argument -> ``$XKERNELS_BACKEND`` -> the per-vendor
-auto order (amd: HIP, TRITON, REFERENCE). Optional backends register inside
-``backend_registration_guard`` so an import failure is recorded (and re-raised
-under ``XKERNELS_STRICT_BACKENDS=1``) instead of breaking the package.
+The interface is the reference's: ``register(kernel, Backend)`` as a decorator
+(src/xkernels/_dispatch.py:90-95), ``dispatch(kernel, *args, backend=..., **kw)``
+(:243-247), ``backend_registration_guard`` for optional backends (:74-87), and
+the resolution order explicit argument -> ``$XKERNELS_BACKEND`` -> the vendor's
+preference list (amd: HIP, TRITON, REFERENCE; :37-41, :162-187).
 
-This package registers only the HIP backend. There is no silent CPU fallback:
-with no backend able to take a call, ``dispatch`` raises.
+Every kernel name owns one ``_Entry``: the callables per backend and the
+registration errors seen for it. Errors are surfaced, never swallowed: an
+explicit request for a backend that failed to register raises ``RuntimeError``
+with the recorded cause, and an automatic choice that had to pass over such a
+backend warns once. This package registers HIP only; nothing falls back to the
+CPU unless a REFERENCE backend was installed (the tests install the oracle).
 """
 from __future__ import annotations
 
 import os
 import warnings
-from collections.abc import Callable
+from collections.abc import Callable, Iterable
 from contextlib import contextmanager
-from dataclasses import dataclass
 
 from ._backends import Backend, detect_vendor
 
-_REGISTRY: dict[str, dict[Backend, Callable]] = {}
-
-
-@dataclass(frozen=True)
-class BackendFailure:
-    kernel_name: str
-    backend: Backend
-    source: str
-    exc_type: str
-    message: str
-    exception: BaseException
-
-
-_BACKEND_FAILURES: dict[str, list[BackendFailure]] = {}
-_FALLBACK_WARNED: set[tuple] = set()
-
-_AUTO_ORDER: dict[str, list[Backend]] = {
-    "nvidia": [Backend.CUDA, Backend.TRITON, Backend.REFERENCE],
-    "amd": [Backend.HIP, Backend.TRITON, Backend.REFERENCE],
-    "none": [Backend.REFERENCE],
+_PREFERENCE: dict[str, tuple[Backend, ...]] = {
+    "amd": (Backend.HIP, Backend.TRITON, Backend.REFERENCE),
+    "nvidia": (Backend.CUDA, Backend.TRITON, Backend.REFERENCE),
+    "none": (Backend.REFERENCE,),
 }
 
-_TRUE = {"1", "true", "yes", "on"}
+
+class _Entry:
+    """Callables and registration errors of one kernel name."""
+
+    __slots__ = ("impls", "errors", "warned")
+
+    def __init__(self) -> None:
+        self.impls: dict[Backend, Callable] = {}
+        self.errors: list[tuple[Backend, str, BaseException]] = []  # (backend, source, exc)
+        self.warned = False
+
+    def error_for(self, backend: Backend) -> tuple[str, BaseException] | None:
+        for b, source, exc in reversed(self.errors):
+            if b is backend:
+                return source, exc
+        return None
 
 
-def _strict() -> bool:
-    return os.environ.get("XKERNELS_STRICT_BACKENDS", "").lower() in _TRUE
+_TABLE: dict[str, _Entry] = {}
 
 
-def _names(kernel_names) -> tuple[str, ...]:
-    return (kernel_names,) if isinstance(kernel_names, str) else tuple(kernel_names)
+def _entry(kernel: str) -> _Entry:
+    e = _TABLE.get(kernel)
+    if e is None:
+        e = _TABLE[kernel] = _Entry()
+    return e
 
 
-def record_backend_failure(kernel_names, backend: Backend, exc: BaseException, *, source: str) -> None:
-    """Remember why an optional backend did not register (see ``backend_diagnostics``)."""
-    for name in _names(kernel_names):
-        _BACKEND_FAILURES.setdefault(name, []).append(
-            BackendFailure(name, backend, source, type(exc).__name__, str(exc), exc)
-        )
-
-
-@contextmanager
-def backend_registration_guard(kernel_names, backend: Backend, *, source: str):
-    """Record (strict mode: re-raise) exceptions raised while registering a backend."""
+def _as_backend(value) -> Backend:
+    if isinstance(value, Backend):
+        return value
     try:
-        yield
-    except Exception as exc:  # noqa: BLE001 - any import/registration error is recorded
-        record_backend_failure(kernel_names, backend, exc, source=source)
-        if _strict():
-            raise
+        return Backend(str(value).strip().lower())
+    except ValueError:
+        raise KeyError(f"unknown backend {value!r}; known: {[b.value for b in Backend]}") from None
 
+
+def _describe(exc: BaseException) -> str:
+    return f"{type(exc).__name__}: {exc}"
+
+
+# ---------------------------------------------------------------- registry ---
 
 def register(kernel_name: str, backend: Backend) -> Callable[[Callable], Callable]:
-    def deco(fn: Callable) -> Callable:
-        _REGISTRY.setdefault(kernel_name, {})[backend] = fn
+    """Decorator: ``fn`` implements ``kernel_name`` on ``backend``."""
+    b = _as_backend(backend)
+
+    def bind(fn: Callable) -> Callable:
+        _entry(kernel_name).impls[b] = fn
         return fn
 
-    return deco
+    return bind
 
 
 def unregister(kernel_name: str, backend: Backend) -> None:
-    """Remove one registration (used by tests that install temporary backends)."""
-    _REGISTRY.get(kernel_name, {}).pop(backend, None)
+    """Removes one binding (tests install temporary backends)."""
+    e = _TABLE.get(kernel_name)
+    if e is not None:
+        e.impls.pop(_as_backend(backend), None)
+
+
+def forget(kernel_name: str) -> None:
+    """Drops every binding and recorded error of ``kernel_name``."""
+    _TABLE.pop(kernel_name, None)
+
+
+def record_backend_failure(kernel_names: str | Iterable[str], backend: Backend,
+                           exc: BaseException, *, source: str) -> None:
+    """Remembers that ``backend`` could not be registered for these kernels."""
+    names = [kernel_names] if isinstance(kernel_names, str) else list(kernel_names)
+    for name in names:
+        _entry(name).errors.append((_as_backend(backend), source, exc))
+
+
+@contextmanager
+def backend_registration_guard(kernel_names: str | Iterable[str], backend: Backend, *,
+                               source: str):
+    """Runs a backend's registration; an exception is recorded for the kernels
+    (and re-raised when ``XKERNELS_STRICT_BACKENDS`` is set to a true value)."""
+    try:
+        yield
+    except Exception as exc:  # noqa: BLE001 - recorded, surfaced at dispatch time
+        record_backend_failure(kernel_names, backend, exc, source=source)
+        if os.environ.get("XKERNELS_STRICT_BACKENDS", "").strip().lower() in ("1", "true", "yes", "on"):
+            raise
 
 
 def registered_backends(kernel_name: str) -> list[Backend]:
-    return list(_REGISTRY.get(kernel_name, {}))
+    e = _TABLE.get(kernel_name)
+    return list(e.impls) if e else []
 
 
 def registered_kernels() -> list[str]:
-    return list(_REGISTRY)
-
-
-def backend_failures(kernel_name: str | None = None) -> dict[str, list[BackendFailure]]:
-    if kernel_name is not None:
-        return {kernel_name: list(_BACKEND_FAILURES.get(kernel_name, ()))}
-    return {k: list(v) for k, v in _BACKEND_FAILURES.items()}
+    return [k for k, e in _TABLE.items() if e.impls]
 
 
 def backend_diagnostics() -> dict[str, dict[str, object]]:
-    """Registered backends and recorded failures for every known kernel."""
-    out: dict[str, dict[str, object]] = {}
-    for name in sorted(set(_REGISTRY) | set(_BACKEND_FAILURES)):
-        out[name] = {
-            "registered": [b.value for b in registered_backends(name)],
-            "failures": [
-                {"backend": f.backend.value, "source": f.source, "type": f.exc_type,
-                 "message": f.message}
-                for f in _BACKEND_FAILURES.get(name, ())
-            ],
+    """Per kernel: the registered backends and the recorded registration errors."""
+    return {
+        name: {
+            "registered": [b.value for b in e.impls],
+            "failures": [{"backend": b.value, "source": src, "type": type(x).__name__,
+                          "message": str(x)} for b, src, x in e.errors],
         }
-    return out
+        for name, e in sorted(_TABLE.items())
+    }
 
 
-def _coerce(backend) -> Backend:
-    return backend if isinstance(backend, Backend) else Backend(str(backend).lower())
+# --------------------------------------------------------------- selection ---
 
-
-def _unregistered(kernel_name: str, backend: Backend, impls: dict) -> Exception:
-    for f in reversed(_BACKEND_FAILURES.get(kernel_name, ())):
-        if f.backend is backend:
-            err = RuntimeError(
-                f"backend {backend.name} failed to register for '{kernel_name}' from "
-                f"{f.source}: {f.exc_type}: {f.message}"
-            )
-            err.__cause__ = f.exception
-            return err
-    return KeyError(
-        f"backend {backend.name} not registered for '{kernel_name}'; have {[b.name for b in impls]}"
-    )
-
-
-def _select_backend_with_source(kernel_name: str, backend="auto") -> tuple[Backend, str]:
-    if kernel_name not in _REGISTRY or not _REGISTRY[kernel_name]:
-        failures = _BACKEND_FAILURES.get(kernel_name)
-        if failures:
-            f = failures[-1]
-            raise RuntimeError(
-                f"no backend registered for '{kernel_name}': {f.backend.name} from {f.source} "
-                f"failed with {f.exc_type}: {f.message}"
-            ) from f.exception
-        raise KeyError(f"no backends registered for kernel '{kernel_name}'")
-    impls = _REGISTRY[kernel_name]
-    if backend != "auto":
-        chosen = _coerce(backend)
-        if chosen not in impls:
-            raise _unregistered(kernel_name, chosen, impls)
-        return chosen, "explicit"
-    env = os.environ.get("XKERNELS_BACKEND")
-    if env:
-        chosen = Backend(env.lower())
-        if chosen in impls:
-            return chosen, "env"
-        raise _unregistered(kernel_name, chosen, impls)
-    for cand in _AUTO_ORDER.get(detect_vendor(), [Backend.REFERENCE]):
-        if cand in impls:
-            return cand, "auto"
-    return next(iter(impls)), "fallback_any"
+def _missing(kernel: str, backend: Backend, e: _Entry | None) -> Exception:
+    failed = e.error_for(backend) if e else None
+    if failed is not None:
+        source, exc = failed
+        err = RuntimeError(f"backend {backend.name} for '{kernel}' failed to register "
+                           f"({source}): {_describe(exc)}")
+        err.__cause__ = exc
+        return err
+    have = [b.name for b in e.impls] if e else []
+    return KeyError(f"backend {backend.name} not registered for '{kernel}'; have {have}")
 
 
 def select_backend(kernel_name: str, backend="auto") -> Backend:
-    return _select_backend_with_source(kernel_name, backend)[0]
+    """The backend a call of ``kernel_name`` runs on."""
+    e = _TABLE.get(kernel_name)
+    if e is None or not e.impls:
+        if e is not None and e.errors:
+            b, source, exc = e.errors[-1]
+            raise RuntimeError(f"no backend registered for '{kernel_name}': {b.name} "
+                               f"({source}) failed with {_describe(exc)}") from exc
+        raise KeyError(f"no backends registered for kernel '{kernel_name}'")
+    if backend != "auto":
+        want = _as_backend(backend)
+        if want not in e.impls:
+            raise _missing(kernel_name, want, e)
+        return want
+    env = os.environ.get("XKERNELS_BACKEND", "").strip()
+    if env:
+        want = _as_backend(env)
+        if want not in e.impls:
+            raise _missing(kernel_name, want, e)
+        return want
+    order = _PREFERENCE.get(detect_vendor(), (Backend.REFERENCE,))
+    for b in order:
+        if b in e.impls:
+            return b
+    return next(iter(e.impls))
 
 
-def _has_cuda_tensor(obj) -> bool:
-    if getattr(obj, "is_cuda", False):
-        return True
-    if isinstance(obj, dict):
-        return any(_has_cuda_tensor(v) for v in obj.values())
-    if isinstance(obj, (list, tuple)):
-        return any(_has_cuda_tensor(v) for v in obj)
-    return False
-
-
-def _warn_reference_fallback(kernel_name, backend, chosen, source, args, kwargs) -> None:
-    # Same policy as the reference (_dispatch.py:204-240): auto picking REFERENCE
-    # for GPU tensors after an optimized backend failed to register is loud.
-    if backend != "auto" or chosen is not Backend.REFERENCE or source != "auto":
+def _warn_if_passed_over(kernel: str, chosen: Backend, args, kwargs) -> None:
+    """An automatic choice of REFERENCE for device tensors after a preferred
+    backend failed to register is reported once (the call still runs)."""
+    e = _TABLE[kernel]
+    if chosen is not Backend.REFERENCE or e.warned:
         return
-    if not (_has_cuda_tensor(args) or _has_cuda_tensor(kwargs)):
+    order = _PREFERENCE.get(detect_vendor(), ())
+    skipped = [(b, *e.error_for(b)) for b in order[:order.index(chosen)] if e.error_for(b)] \
+        if chosen in order else []
+    if not skipped:
         return
-    failures = [f for f in _BACKEND_FAILURES.get(kernel_name, ()) if f.backend is not Backend.REFERENCE]
-    if not failures:
+    on_device = any(getattr(a, "is_cuda", False) for a in (*args, *kwargs.values()))
+    if not on_device:
         return
-    key = (kernel_name, tuple((f.backend.value, f.source, f.message) for f in failures))
-    if key in _FALLBACK_WARNED:
-        return
-    _FALLBACK_WARNED.add(key)
-    summary = "; ".join(f"{f.backend.value} from {f.source}: {f.exc_type}: {f.message}" for f in failures)
-    warnings.warn(
-        f"backend='auto' selected REFERENCE for '{kernel_name}' on a GPU tensor after "
-        f"optimized backend registration failed ({summary})",
-        RuntimeWarning,
-        stacklevel=3,
-    )
+    e.warned = True
+    why = "; ".join(f"{b.value} ({src}): {_describe(x)}" for b, src, x in skipped)
+    warnings.warn(f"backend='auto' selected REFERENCE for '{kernel}' on device tensors because "
+                  f"a preferred backend failed to register: {why}", RuntimeWarning, stacklevel=3)
 
 
 def dispatch(kernel_name: str, *args, backend="auto", **kwargs):
-    """Run ``kernel_name`` on the selected backend."""
-    chosen, source = _select_backend_with_source(kernel_name, backend)
-    _warn_reference_fallback(kernel_name, backend, chosen, source, args, kwargs)
-    return _REGISTRY[kernel_name][chosen](*args, **kwargs)
+    """Runs ``kernel_name`` on the selected backend."""
+    chosen = select_backend(kernel_name, backend)
+    if backend == "auto" and not os.environ.get("XKERNELS_BACKEND", "").strip():
+        _warn_if_passed_over(kernel_name, chosen, args, kwargs)
+    return _TABLE[kernel_name].impls[chosen](*args, **kwargs)

@@ -9,15 +9,15 @@ from typing import Any
 from .registry import all_specs, cards_for
 from .registry.archs import vendor_of
 from .registry.constraints import UndecidableConstraintError, evaluate
-from .registry.models import ImplCard, OpSpec
+from .registry.catalog import ImplCard, OpSpec
 
 
 def _arch_reasons(card: ImplCard, target: str, features: set[str]) -> list[str]:
     r: list[str] = []
-    fam = card.arch.family
+    fam = card.arch_family
     if fam != "any" and fam != target:
         r.append(f"arch.family {fam!r} != target {target!r}")
-    r += [f"missing required feature {x!r}" for x in card.arch.requires if x not in features]
+    r += [f"missing required feature {x!r}" for x in card.arch_requires if x not in features]
     if card.backend.name == "CUDA" and vendor_of(target) == "amd":
         r.append("cuda backend on an amd target")
     if card.backend.name == "HIP" and vendor_of(target) == "nvidia":
@@ -54,7 +54,7 @@ def _matched(card: ImplCard, specs: dict[str, dict], arch: str):
     dtype = next((q["dtype"] for q in specs.values() if q.get("dtype")), None)
     if dtype is None:
         return None
-    return next((m for m in card.measured if m.arch == arch and m.dtype == dtype), None)
+    return next((m for m in card.measured if m["arch"] == arch and m["dtype"] == dtype), None)
 
 
 def _score(card: ImplCard, ok: bool, matched, objective: str) -> float:
@@ -102,8 +102,9 @@ def find_impl(canonical_op: str, input_specs: dict[str, dict] | None = None,
                 "arch": target_arch, "applicable": ok, "reject_reasons": reasons,
                 "score": _score(card, ok, m, objective),
                 "matched_measurement": None if m is None else {
-                    "arch": m.arch, "shape": dict(m.shape), "dtype": m.dtype, "tflops": m.tflops,
-                    "ms": m.ms, "achieved_bw_pct": m.achieved_bw_pct, "source": m.source},
+                    "arch": m["arch"], "shape": dict(m["shape"]), "dtype": m["dtype"],
+                    "tflops": m.get("tflops"), "ms": m.get("ms"),
+                    "achieved_bw_pct": m.get("achieved_bw_pct"), "source": m["source"]},
             })
         if not op_rej and not any_ok:
             results[-1]["missing_backend"] = True

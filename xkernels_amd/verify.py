@@ -22,7 +22,7 @@ import torch
 from .registry import backend_callable, get_card, get_spec, load_shape_sweep, reference_callable
 from .registry.archs import vendor_of
 from .registry.input_gen import generate_inputs
-from .registry.models import ImplCard, OpSpec
+from .registry.catalog import ImplCard, OpSpec
 
 DEFAULT_SEED = 1729
 
@@ -132,11 +132,11 @@ def verify(impl_card_id: str, arch: str = "any", *, knobs: dict | None = None, s
             outs.append((p, ref, _normalize(got)))
         try:
             again = _normalize(_run(card, op, points[0], seed, device, knobs))
-            determinism = _errors(again, outs[0][2])[1] <= op.numerics.rtol
+            determinism = _errors(again, outs[0][2])[1] <= op.rtol
         except Exception:  # noqa: BLE001
             determinism = False
         for p, ref, got in outs:
-            rtol, atol = op.numerics.tolerance_for(p.get("dtype", "fp32"))
+            rtol, atol = op.tolerance(p.get("dtype", "fp32"))
             a, r = _errors(got, ref)
             mabs, mrel = max(mabs, a), max(mrel, r)
             if not _within(got, ref, rtol, atol):
@@ -178,7 +178,7 @@ def _measure_perf(card: ImplCard, op: OpSpec, point: dict, seed: int, device: st
     model = cost_model(op.id, point)
     if model is not None:
         flops, nbytes = model
-        arch = card.arch.family if card.arch.family != "any" else "any"
+        arch = card.arch_family
         peaks = arch_peaks(arch)
         if ms > 0 and flops > 0 and peaks["fp32_tflops"] > 0:
             tflops = round(flops / (ms * 1e-3) / 1e12, 3)
@@ -219,14 +219,14 @@ def verify_parity(op_id: str, archs: list[str] | None = None, *, shapes=None,
         for j in range(i + 1, len(names)):
             a, b = names[i], names[j]
             for idx, (oa, ob) in enumerate(zip(outputs[a], outputs[b], strict=True)):
-                _, atol = op.numerics.tolerance_for(points[idx].get("dtype", "fp32"))
+                _, atol = op.tolerance(points[idx].get("dtype", "fp32"))
                 ae, re_ = _errors(oa, ob)
                 worst = max(worst, re_)
-                if not _within(oa, ob, op.numerics.cross_backend_rtol, atol):
+                if not _within(oa, ob, op.cross_backend_rtol, atol):
                     diverging.append({"pair": [a, b], "point": points[idx], "abs_err": ae, "rel_err": re_})
     inconclusive = len(names) < 2
     return {
-        "op_id": op_id, "cross_backend_rtol": op.numerics.cross_backend_rtol, "device": device,
+        "op_id": op_id, "cross_backend_rtol": op.cross_backend_rtol, "device": device,
         "agree": None if inconclusive else not diverging, "inconclusive": inconclusive,
         "n_runnable": len(names), "max_pairwise_rel_err": worst, "diverging": diverging,
         "per_backend_runnable": {k: k in outputs for k in cards_for(op_id)}, "errors": errors,
