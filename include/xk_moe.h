@@ -55,21 +55,10 @@ extern "C" {
 /* int4 flags. Default (0): every dequantised weight is rounded to bf16 before
  * the contraction, as the reference does. XK_INT4_FAST_DEQUANT contracts the
  * exact (nibble-8)*scale product instead (cheaper unpack; differs from the
- * reference by the reference's own bf16 rounding of the weights). */
+ * reference by the reference's own bf16 rounding of the weights) where the
+ * decode K-split kernel takes the shape, and is ignored elsewhere. Other bits
+ * are reserved. */
 #define XK_INT4_FAST_DEQUANT 1
-/* Diagnostic: force the non-persistent stream kernels (also used when K is not
- * a multiple of 256). */
-#define XK_INT4_V1 2
-/* Kernel choice for bf16 / group-32 inputs. By default the MFMA tile kernel
- * (prefill regime) runs when numel >= 64 * E and the shapes allow it (K a
- * multiple of 256, N of 256), else the weight-streaming kernel (decode regime).
- * These flags force one or the other where the shapes allow it; the tile
- * kernel always uses the reference's bf16-rounded weights. */
-#define XK_INT4_FORCE_TILE 4
-#define XK_INT4_FORCE_STREAM 8
-/* Diagnostic: with XK_INT4_FAST_DEQUANT, use the column-split persistent
- * stream kernel instead of the K-split decode kernel. */
-#define XK_INT4_V2 16
 
 /* Message of the last failed call on this thread ("" if none). */
 const char* xk_last_error(void);

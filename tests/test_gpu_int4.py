@@ -162,26 +162,3 @@ def test_fast_dequant_config2(dev):
     A, packed, scale, ids, w = _device_case(64, 48, 4096, 7168, 8, ids, 20)
     got = moe_int4_w4a16_hip(A, packed, scale, ids, w, exact_dequant=False)
     assert_close(got, moe_w4a16_ref(A, packed, scale, ids, w), 2e-2, 2e-2, "C2 fast")
-
-
-def test_persistent_and_grid_kernels_agree(dev):
-    """The persistent kernel (K % 256 == 0) and the per-expert grid kernels see the
-    same inputs; both match the oracle (v1 forced with the diagnostic flag)."""
-    from xkernels_amd import _lib
-
-    A, packed, scale, ids, w = _case(24, 12, 384, 768, 4)
-    d = [t.to(dev) for t in (A, packed, scale, ids, w)]
-    M, K = A.shape
-    E, N, _ = packed.shape
-    outs = []
-    for flags in (0, _lib.XK_INT4_V1):
-        out = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
-        nb = _lib.query("xk_moe_int4_w4a16_workspace_bytes", M, 4, E, N, K)
-        ws = torch.empty(nb, dtype=torch.uint8, device=dev)
-        _lib.call("xk_moe_int4_w4a16", d[0].data_ptr(), _lib.XK_DT_BF16, M, K, d[1].data_ptr(),
-                  d[2].data_ptr(), E, N, 32, d[3].data_ptr(), d[4].data_ptr(), 4, None, 0, 1, flags,
-                  out.data_ptr(), ws.data_ptr(), ws.numel(), torch.cuda.current_stream().cuda_stream)
-        outs.append(out)
-    want = moe_w4a16_ref(A, packed, scale, ids, w)
-    for o in outs:
-        assert_close(o, want, 2e-2, 2e-2, "kernel variant")

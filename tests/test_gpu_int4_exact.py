@@ -92,11 +92,13 @@ def _device_inputs(M, E, N, K, ids, seed):
     (40, 6, 160, 768, 3, "zipf"),          # K / 256 odd: one-tile passes only
     (5, 4, 96, 512, 2, "uniform"),         # N not a multiple of 128
     (1024, 8, 512, 1024, 4, "zipf"),       # prefill regime: the MFMA tile kernel
+    (4096, 48, 4096, 7168, 8, "zipf"),     # C5 at full size, every row (tile kernel)
 ])
 def test_rows_within_fp32_summation_error(M, E, N, K, top_k, routing):
     if not torch.cuda.is_available():
         pytest.skip("no GPU")
     ids = uniform_topk(M, top_k, E, 3) if routing == "uniform" else zipf_topk(M, top_k, E, 1.2, 3)
+    print(f"case M={M} E={E} N={N} K={K} top_k={top_k} {routing}", flush=True)
     A, packed, scale, ids = _device_inputs(M, E, N, K, ids, 11)
     rows = _gemm_rows(A, packed, scale, ids)
     assert not torch.isnan(rows).any(), "a routed slot's row was not written"

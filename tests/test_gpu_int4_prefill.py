@@ -55,11 +55,12 @@ def _slot_rows(A, packed, scale, ids, flags):
     _lib.call("xk_moe_align_block_size", ids.data_ptr(), numel, E, bs, None, 0, sorted_ids.data_ptr(),
               expert_ids.data_ptr(), num_post.data_ptr(), offsets.data_ptr(), ws.data_ptr(), ws.numel(),
               _stream())
-    slot_out = torch.full((1, numel, N), float("nan"), dtype=torch.float32, device=dev)
+    parts = _lib.query("xk_moe_int4_gemm_parts", M, k, E, N, K, _lib.XK_DT_BF16, 32, flags)
+    slot_out = torch.full((parts, numel, N), float("nan"), dtype=torch.float32, device=dev)
     _lib.call("xk_moe_int4_w4a16_gemm", A.data_ptr(), _lib.XK_DT_BF16, M, K, packed.data_ptr(),
               scale.data_ptr(), E, N, 32, ids.data_ptr(), k, None, 0, sorted_ids.data_ptr(),
               offsets.data_ptr(), slot_out.data_ptr(), flags, None, 0, _stream())
-    return slot_out[0]
+    return slot_out.sum(0)
 
 
 def _inputs(M, E, N, K, ids, seed, scale_hi=0.02):
@@ -84,8 +85,8 @@ def test_tile_kernel_rows_match_stream_kernel(M, E, N, K, top_k, routing, dev):
     print(f"tile vs stream M={M} E={E} N={N} K={K} k={top_k} {routing}", flush=True)
     ids = zipf_topk(M, top_k, E, 1.2, M) if routing == "zipf" else uniform_topk(M, top_k, E, M)
     A, packed, scale, ids, _ = _inputs(M, E, N, K, ids, seed=M + 3)
-    tile = _slot_rows(A, packed, scale, ids, _lib.XK_INT4_FORCE_TILE)
-    stream = _slot_rows(A, packed, scale, ids, _lib.XK_INT4_FORCE_STREAM)
+    tile = _slot_rows(A, packed, scale, ids, _lib._XK_INT4_TEST_FORCE_TILE)
+    stream = _slot_rows(A, packed, scale, ids, _lib._XK_INT4_TEST_FORCE_STREAM)
     torch.cuda.synchronize()
     assert not torch.isnan(tile).any(), "a routed slot row was not written"
     assert_close(tile, stream, 1e-4, 1e-4 * float(stream.abs().mean()), "tile vs stream rows")
@@ -96,7 +97,7 @@ def test_tile_kernel_matches_oracle(M, E, N, K, top_k, routing, dev):
     print(f"tile vs oracle M={M} E={E} N={N} K={K} k={top_k} {routing}", flush=True)
     ids = zipf_topk(M, top_k, E, 1.2, M + 1) if routing == "zipf" else uniform_topk(M, top_k, E, M + 1)
     A, packed, scale, ids, w = _inputs(M, E, N, K, ids, seed=M + 5)
-    got = _fused(A, packed, scale, ids, w, _lib.XK_INT4_FORCE_TILE)
+    got = _fused(A, packed, scale, ids, w, _lib._XK_INT4_TEST_FORCE_TILE)
     assert_close(got, moe_w4a16_ref(A, packed, scale, ids, w), 2e-2, 2e-2, "tile fused")
 
 
@@ -104,7 +105,7 @@ def test_tile_kernel_unweighted_and_expert_parallel(dev):
     M, E, N, K, k = 512, 16, 512, 1024, 4
     ids = zipf_topk(M, k, E, 1.1, 77)
     A, packed, scale, ids, w = _inputs(M, E, N, K, ids, seed=78)
-    got = _fused(A, packed, scale, ids, w, _lib.XK_INT4_FORCE_TILE, mul=0)
+    got = _fused(A, packed, scale, ids, w, _lib._XK_INT4_TEST_FORCE_TILE, mul=0)
     assert_close(got, moe_w4a16_ref(A, packed, scale, ids, w, mul_routed_weight=False), 2e-2, 2e-2,
                  "tile unweighted")
     dense = moe_w4a16_ref(A, packed, scale, ids, w).float()
@@ -113,7 +114,7 @@ def test_tile_kernel_unweighted_and_expert_parallel(dev):
         emap = torch.full((E,), -1, dtype=torch.int32, device="cuda")
         emap[r * 8:(r + 1) * 8] = torch.arange(8, dtype=torch.int32, device="cuda")
         lp, ls = packed[r * 8:(r + 1) * 8].contiguous(), scale[r * 8:(r + 1) * 8].contiguous()
-        part = _fused(A, lp, ls, ids, w, _lib.XK_INT4_FORCE_TILE, emap=emap)
+        part = _fused(A, lp, ls, ids, w, _lib._XK_INT4_TEST_FORCE_TILE, emap=emap)
         total += part.float()
     assert_close(total, dense, 3e-2, 3e-2, "tile EP partials")
 
@@ -125,5 +126,5 @@ def test_default_choice_uses_tile_kernel_at_prefill_sizes(dev):
     ids = zipf_topk(M, k, E, 1.2, 5)
     A, packed, scale, ids, _ = _inputs(M, E, N, K, ids, seed=6)
     default = _slot_rows(A, packed, scale, ids, 0)
-    tile = _slot_rows(A, packed, scale, ids, _lib.XK_INT4_FORCE_TILE)
+    tile = _slot_rows(A, packed, scale, ids, _lib._XK_INT4_TEST_FORCE_TILE)
     assert torch.equal(default, tile)

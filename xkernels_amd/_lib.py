@@ -11,6 +11,7 @@ import ctypes
 import os
 from pathlib import Path
 
+ROOT_CSRC = Path(__file__).resolve().parent / "csrc"
 LIB_PATH = Path(os.environ.get("XK_MOE_LIB", Path(__file__).resolve().parent / "_lib" / "libxk_moe.so"))
 
 XK_OK = 0
@@ -21,10 +22,10 @@ XK_DT_BF16 = 0
 XK_DT_FP32 = 1
 XK_DT_NONE = -1
 XK_INT4_FAST_DEQUANT = 1
-XK_INT4_V1 = 2
-XK_INT4_FORCE_TILE = 4
-XK_INT4_FORCE_STREAM = 8
-XK_INT4_V2 = 16
+# Test-only bits of the int4 flags (csrc/int4_flags.h; not part of the ABI):
+# pick the tile or the stream kernel where the shapes allow both.
+_XK_INT4_TEST_FORCE_TILE = 1 << 8
+_XK_INT4_TEST_FORCE_STREAM = 1 << 9
 
 _p = ctypes.c_void_p
 _i32 = ctypes.c_int32
