@@ -10,7 +10,12 @@ the ``roofline`` object. ``cpu_baseline`` times the CPU oracle (the reference
 backend's literal per-(token, expert) loop restated in torch) on the host cores
 on the full batch.
 
+The same step is also captured once into a HIP graph (``torch.cuda.CUDAGraph``,
+address-stable workspace) and replayed; its time is reported beside the eager
+one as ``ms_per_step_graph`` (``value`` stays the eager rate).
+
     python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--no-cpu] [--fast-dequant]
+    python bench.py --workload {c3-align,c3-reduce,c4,c5,f1-down} [--m M]   (secondary lines)
 """
 from __future__ import annotations
 
@@ -38,29 +43,29 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--fast-dequant", action="store_true",
                     help="exact (n-8)*s contraction instead of the reference's bf16-rounded weights")
     ap.add_argument("--seed", type=int, default=20)
-    ap.add_argument("--workload", default="c2", choices=["c2", "c3-align", "c3-reduce", "c4", "c5"],
+    ap.add_argument("--workload", default="c2",
+                    choices=["c2", "c3-align", "c3-reduce", "c4", "c5", "f1-down"],
                     help="c2 is the headline line; the others time the other BASELINE configs' "
-                         "kernels (secondary lines, not the headline metric)")
+                         "kernels and the layer's down projection (secondary lines, not the "
+                         "headline metric)")
+    ap.add_argument("--m", type=int, default=64, help="tokens for --workload f1-down")
     ap.add_argument("--profile-only", action="store_true",
                     help="run warmup + timed steps only (for rocprofv3), print nothing else")
     ap.add_argument("--gemm-only", action="store_true",
                     help="with --profile-only: launch only the grouped GEMM (for --pmc passes)")
-    ap.add_argument("--extra-flags", type=int, default=0,
-                    help="diagnostic: XK_INT4_* bits OR-ed into the GEMM flags")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run 5 device copies of 1 GiB and exit (calibrates FETCH_SIZE/WRITE_SIZE)")
     return ap.parse_args()
 
 
-def make_inputs(seed: int):
-    """C2: bf16 A ~ N(0,1); uint4 weights U[0,15] (zero point 8) packed in int32;
-    bf16 scales U(0.005, 0.02); 8 distinct uniform experts per token; softmax
-    routing weights of Gaussian logits."""
+def make_inputs(seed: int, M: int = 64, E: int = 48, N: int = 4096, K: int = 7168, top_k: int = 8):
+    """C2 by default: bf16 A ~ N(0,1); uint4 weights U[0,15] (zero point 8) packed
+    in int32; bf16 scales U(0.005, 0.02); top_k distinct uniform experts per
+    token; softmax routing weights of Gaussian logits."""
     import torch
 
     from xkernels_amd import make_w4a16_weights
 
-    M, E, N, K, top_k = 64, 48, 4096, 7168, 8
     packed, scale, _ = make_w4a16_weights(E, N, K, 32, device="cuda", seed=seed, scale_hi=0.02)
     g = torch.Generator().manual_seed(seed + 1)
     A = torch.randn(M, K, generator=g).to(torch.bfloat16).cuda()
@@ -114,6 +119,40 @@ def time_gemm_kernel(c, flags: int, iters: int) -> float:
     return sum(d) / len(d)
 
 
+def int4_step(c, exact: bool):
+    """One fused call on the inputs ``c`` with an address-stable workspace."""
+    import torch
+
+    from xkernels_amd import Backend, MoeInt4Workspace, fused_moe_int4_w4a16
+    from xkernels_amd.moe.hip_backend import moe_int4_w4a16_hip
+
+    ws = MoeInt4Workspace.allocate(c["M"], c["top_k"], c["N"], dtype=torch.bfloat16,
+                                   device="cuda", num_experts=c["E"], K=c["K"])
+    if exact:  # the public op, default (reference-rounded) dequant
+        return lambda: fused_moe_int4_w4a16(c["A"], c["packed"], c["scale"], c["ids"], c["w"],
+                                            backend=Backend.HIP, workspace=ws)
+    # the knob is a backend specialization (Impl Card knob), not a public kwarg
+    return lambda: moe_int4_w4a16_hip(c["A"], c["packed"], c["scale"], c["ids"], c["w"],
+                                      workspace=ws, exact_dequant=False)
+
+
+def graph_time(step, steps: int, warmup: int) -> float:
+    """Average ms per replay of ``step`` captured once into a HIP graph."""
+    import torch
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        step()
+    return _event_time(g.replay, steps, warmup)
+
+
 COPY_BYTES = 1 << 30
 
 
@@ -130,7 +169,8 @@ def copy_calibration() -> int:
     return 0
 
 
-TRAFFIC_FILE = ROOT / "profiles" / "int4_stream_v2_C2_traffic.json"
+TRAFFIC_FILE = ROOT / "profiles" / "int4_stream_rne_C2_traffic.json"
+KERNEL = {True: "int4_stream_rne", False: "int4_decode_ksplit"}  # exact dequant -> kernel name
 
 
 def measured_traffic(exact: bool) -> dict | None:
@@ -238,6 +278,28 @@ def secondary(a) -> dict:
                 "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
                              "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
                              "algorithmic_bytes": nbytes}}
+    if a.workload == "f1-down":
+        # the layer's down projection: N=7168 (hidden), K=2048 (intermediate), E=48
+        from xkernels_amd import _lib
+
+        exact = not a.fast_dequant
+        c = make_inputs(a.seed, M=a.m, E=48, N=7168, K=2048, top_k=8)
+        e_active = int(torch.unique(c["ids"]).numel())
+        nbytes = int4_weight_bytes(e_active, 7168, 2048)
+        step = int4_step(c, exact)
+        ms = _event_time(step, a.steps, a.warmup)
+        graph_ms = graph_time(step, a.steps, a.warmup)
+        gemm_ms = time_gemm_kernel(c, 0 if exact else _lib.XK_INT4_FAST_DEQUANT, a.gemm_iters)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        kbs = nbytes / (gemm_ms * 1e-3) / 1e9
+        return {"metric": f"moe_int4_w4a16 µs + HBM GB/s at M={a.m},E=48,N=7168,K=2048,top_k=8",
+                "value": round(gbs, 1), "unit": "GB/s", "higher_is_better": True,
+                "us_per_call": round(ms * 1e3, 2), "us_per_call_graph": round(graph_ms * 1e3, 2),
+                "config": {"workload": f"int4 down projection M={a.m}", "E_active": e_active,
+                           "dequant": "bf16-rounded (reference)" if exact else "exact fp32 (fast)"},
+                "roofline": {"bound": "hbm", "kernel": KERNEL[exact], "achieved": round(kbs, 1),
+                             "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(kbs / HBM_PEAK_GBS, 4),
+                             "avg_launch_us": round(gemm_ms * 1e3, 3), "algorithmic_bytes": nbytes}}
     # c5: prefill, contraction bound
     M, E, N, K, k = 4096, 48, 4096, 7168, 8
     packed, scale, _ = make_w4a16_weights(E, N, K, 32, device="cuda", seed=a.seed, scale_hi=0.02)
@@ -263,7 +325,7 @@ def cpu_baseline(c) -> dict:
 
     from oracle.torch_ref import moe_w4a16_ref_loop
 
-    threads = min(os.cpu_count() or 1, 16)
+    threads = os.cpu_count() or 1
     torch.set_num_threads(threads)
     args = [c[k].cpu() for k in ("A", "packed", "scale", "ids", "w")]
     runs = []
@@ -297,8 +359,7 @@ def main() -> int:
         return 2
     import torch
 
-    from xkernels_amd import Backend, MoeInt4Workspace, _lib, fused_moe_int4_w4a16
-    from xkernels_amd.moe.hip_backend import moe_int4_w4a16_hip
+    from xkernels_amd import _lib
     from xkernels_amd.registry.cost_model import int4_weight_bytes
 
     if not torch.cuda.is_available():
@@ -315,19 +376,10 @@ def main() -> int:
         return 0
     c = make_inputs(a.seed)
     exact = not a.fast_dequant
-    flags = (0 if exact else _lib.XK_INT4_FAST_DEQUANT) | a.extra_flags
+    flags = 0 if exact else _lib.XK_INT4_FAST_DEQUANT
     e_active = int(torch.unique(c["ids"]).numel())
     weight_bytes = int4_weight_bytes(e_active, c["N"], c["K"])
-    ws = MoeInt4Workspace.allocate(c["M"], c["top_k"], c["N"], dtype=torch.bfloat16,
-                                   device="cuda", num_experts=c["E"], K=c["K"])
-
-    def step():
-        if exact:  # the public op, default (reference-rounded) dequant
-            return fused_moe_int4_w4a16(c["A"], c["packed"], c["scale"], c["ids"], c["w"],
-                                        backend=Backend.HIP, workspace=ws)
-        # the knob is a backend specialization (Impl Card knob), not a public kwarg
-        return moe_int4_w4a16_hip(c["A"], c["packed"], c["scale"], c["ids"], c["w"],
-                                  workspace=ws, exact_dequant=False)
+    step = int4_step(c, exact)
 
     if a.profile_only and a.gemm_only:
         time_gemm_kernel(c, flags, a.steps)
@@ -347,6 +399,7 @@ def main() -> int:
     if a.profile_only:
         return 0
 
+    graph_ms = graph_time(step, a.steps, a.warmup)
     gemm_ms = time_gemm_kernel(c, flags, a.gemm_iters)
     achieved = weight_bytes / (gemm_ms * 1e-3) / 1e9
     gbs = weight_bytes / (ms * 1e-3) / 1e9
@@ -359,6 +412,7 @@ def main() -> int:
         "warmup": a.warmup,
         "ms_per_step": round(ms, 5),
         "us_per_call": round(ms * 1e3, 2),
+        "ms_per_step_graph": round(graph_ms, 5),
         "pct_of_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
         "higher_is_better": True,
         "scaling": "weak",
@@ -371,7 +425,7 @@ def main() -> int:
                    "dequant": "bf16-rounded (reference)" if exact else "exact fp32 (fast)",
                    "wall_s_timed_region": round(wall, 4)},
         "roofline": {"bound": "hbm",
-                     "kernel": "int4_stream_v2<Int4Mode::%s>" % ("kRne" if exact else "kFast"),
+                     "kernel": KERNEL[exact],
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "avg_launch_us": round(gemm_ms * 1e3, 3),

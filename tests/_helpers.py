@@ -37,3 +37,24 @@ def assert_close(got: torch.Tensor, want: torch.Tensor, rtol: float, atol: float
             f"(rtol={rtol}, atol={atol}); first at {i}: got {got.reshape(-1)[i]:.6g} "
             f"want {want.reshape(-1)[i]:.6g}; max abs err {(got - want).abs().max():.3g}"
         )
+
+
+def bf16_ulp(x: torch.Tensor) -> torch.Tensor:
+    """Spacing of bf16 values at |x| (8 significant bits), floored at the
+    smallest normal's spacing."""
+    a = x.detach().float().abs().clamp_min(2.0 ** -126)
+    return torch.exp2(torch.floor(torch.log2(a)) - 7)
+
+
+def assert_within_bf16_ulps(got: torch.Tensor, want: torch.Tensor, ulps: float, msg: str = ""):
+    """|got - want| <= ulps * (bf16 spacing at want), element by element."""
+    got, want = got.detach().float().cpu(), want.detach().float().cpu()
+    assert got.shape == want.shape, (got.shape, want.shape, msg)
+    err = (got - want).abs()
+    lim = ulps * bf16_ulp(want)
+    bad = ~(err <= lim)
+    if bad.any():
+        i = int(bad.reshape(-1).nonzero()[0])
+        raise AssertionError(f"{msg}: {int(bad.sum())}/{bad.numel()} elements beyond {ulps} bf16 ulp; "
+                             f"first at {i}: got {got.reshape(-1)[i]:.8g} want {want.reshape(-1)[i]:.8g}; "
+                             f"max err in ulps {float((err / bf16_ulp(want)).max()):.3g}")

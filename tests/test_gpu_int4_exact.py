@@ -88,6 +88,8 @@ def _device_inputs(M, E, N, K, ids, seed):
     (64, 48, 4096, 7168, 8, "uniform"),    # C2, the headline (most experts one 16-row tile)
     (16, 8, 1024, 2048, 2, "uniform"),     # C1
     (64, 48, 7168, 2048, 8, "uniform"),    # the down projection of the same layer
+    (16, 48, 7168, 2048, 8, "uniform"),    # ... at M = 16 and M = 1
+    (1, 48, 7168, 2048, 8, "uniform"),
     (192, 16, 512, 1024, 4, "zipf"),       # experts with several 32-row passes
     (40, 6, 160, 768, 3, "zipf"),          # K / 256 odd: one-tile passes only
     (5, 4, 96, 512, 2, "uniform"),         # N not a multiple of 128

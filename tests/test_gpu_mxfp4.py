@@ -145,3 +145,13 @@ def test_config4_full_size(dev):
     assert rel_l2 < 2e-3, rel_l2
     scale = float(want.abs().mean())
     assert_close(got, want, 2e-2, 2e-2 * scale, "C4 vs output scale")
+
+
+def test_known_answer_clamp_and_bias(dev):
+    """The hand-computed answer of tests/_mxfp4_kat.py: one-sided gate clamp,
+    two-sided up clamp, b13 before the clamp, b2 before the routing weight."""
+    from tests import _mxfp4_kat as kat
+    x = {k: (v.to(dev) if torch.is_tensor(v) else v) for k, v in kat.inputs().items()}
+    out = fused_moe_mxfp4(x["A"], *(x[k] for k in KEYS), x["topk_ids"], x["topk_w"], b13=x["b13"],
+                          b2=x["b2"], swiglu_limit=x["swiglu_limit"], backend=Backend.HIP)
+    kat.check(out)

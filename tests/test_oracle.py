@@ -295,3 +295,16 @@ def test_mxfp4_ref_limit_none_equals_huge_limit_and_ep():
         total += R.moe_mxfp4_ref(A.float(), *local, ids, w, swiglu_limit=None, expert_map=emap)
     torch.testing.assert_close(total, R.moe_mxfp4_ref(A.float(), *(wts[x] for x in keys), ids, w,
                                                       swiglu_limit=None), rtol=1e-5, atol=1e-5)
+
+
+def test_mxfp4_ref_known_answer_clamp_and_bias():
+    """Hand-computed values pin the one-sided gate clamp, the two-sided up
+    clamp, b13 before the clamp and b2 before the routing weight (see
+    tests/_mxfp4_kat.py for the arithmetic)."""
+    from tests import _mxfp4_kat as kat
+    x = kat.inputs()
+    kat.check(R.moe_mxfp4_ref(x["A"], x["w13"], x["w13_scale"], x["w2"], x["w2_scale"], x["topk_ids"],
+                              x["topk_w"], b13=x["b13"], b2=x["b2"], swiglu_limit=x["swiglu_limit"]))
+    c = c_oracle.mxfp4_moe(x["A"], x["w13"], x["w13_scale"], x["w2"], x["w2_scale"], x["topk_ids"],
+                           x["topk_w"], b13=x["b13"], b2=x["b2"], swiglu_limit=x["swiglu_limit"])
+    kat.check(c.to(torch.bfloat16))

@@ -58,7 +58,10 @@ def _moe_mxfp4(p: dict[str, Any], seed: int, device: str) -> dict[str, Any]:
     hidden, ispp = int(p["hidden"]), int(p["ispp"])
     bias = bool(p.get("bias", False))
     A = _randn(device, dt, M, hidden, seed=seed)
-    wts = make_mxfp4_moe_weights(E, hidden, ispp, with_bias=bias, device=device, seed=seed + 1)
+    if "a_scale" in p:  # optional input scale of a sweep point
+        A = (A.float() * float(p["a_scale"])).to(dt)
+    sc = {k: int(p[k]) for k in ("scale_lo", "scale_hi") if k in p}  # e8m0 bytes [lo, hi)
+    wts = make_mxfp4_moe_weights(E, hidden, ispp, with_bias=bias, device=device, seed=seed + 1, **sc)
     g = torch.Generator(device=device).manual_seed(seed + 2)
     ids = torch.stack([torch.randperm(E, generator=g, device=device)[:k] for _ in range(M)]).to(torch.int32)
     logits = torch.randn(M, k, generator=g, device=device, dtype=torch.float32)
