@@ -120,6 +120,24 @@ int xk_moe_int4_w4a16(const void* A, int32_t a_dtype, int64_t M, int64_t K,
                       int32_t mul_routed_weight, int32_t flags, void* out,
                       void* workspace, int64_t workspace_bytes, hipStream_t stream);
 
+/* No counterpart in the reference. xk_moe_int4_w4a16 for callers that cannot
+ * allocate device memory (code under HIP graph capture that must not call
+ * hipMalloc, tight serving loops, harnesses that forbid allocation): same
+ * arguments without the workspace; the scratch is a fixed device array of
+ * xk_moe_int4_w4a16_noalloc_max_bytes() bytes (64 MiB) inside the library,
+ * one per GPU, held until the process ends. A call whose
+ * xk_moe_int4_w4a16_workspace_bytes(...) exceeds it fails with XK_ERR_INVALID.
+ * Every call on one GPU uses the same array: calls that overlap on a GPU (two
+ * streams, two host threads) race; calls ordered on one stream do not. */
+int64_t xk_moe_int4_w4a16_noalloc_max_bytes(void);
+int xk_moe_int4_w4a16_noalloc(const void* A, int32_t a_dtype, int64_t M, int64_t K,
+                              const int32_t* packed, const uint16_t* scale, int64_t E,
+                              int64_t N, int32_t group_size, const int32_t* topk_ids,
+                              const float* topk_w, int64_t top_k,
+                              const int32_t* expert_map, int32_t num_global_experts,
+                              int32_t mul_routed_weight, int32_t flags, void* out,
+                              hipStream_t stream);
+
 /* Stage entry point: only the grouped INT4 GEMM (the reference's
  * _fused_moe_int4_kernel launch, moe_int4_kernel.py:78-272). Consumes the
  * align outputs built with block_size = xk_moe_int4_block_size(M, top_k, E)

@@ -48,6 +48,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [_p, _i32, _i64, _i64, _p, _p, _i64, _i64, _i32, _p, _p, _i64, _p, _i32, _i32, _i32, _p,
          _p, _i64, _p],
     ),
+    "xk_moe_int4_w4a16_noalloc_max_bytes": (_i64, []),
+    "xk_moe_int4_w4a16_noalloc": (
+        ctypes.c_int,
+        [_p, _i32, _i64, _i64, _p, _p, _i64, _i64, _i32, _p, _p, _i64, _p, _i32, _i32, _i32, _p, _p],
+    ),
     "xk_moe_int4_block_size": (_i32, [_i64, _i64, _i64]),
     "xk_moe_int4_w4a16_gemm": (
         ctypes.c_int,

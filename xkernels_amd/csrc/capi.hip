@@ -2,11 +2,14 @@
 //
 // Argument checks happen here, before any launch, so a bad shape is reported as
 // XK_ERR_INVALID instead of reaching a kernel. Pipelines carve their scratch
-// from the caller's workspace; nothing is allocated here.
+// from the caller's workspace; nothing is allocated here. The one exception to
+// "the caller brings the workspace" is xk_moe_int4_w4a16_noalloc, whose scratch
+// is a fixed device array of this library (see below).
 #include <stdarg.h>
 #include <stdio.h>
 
 #include <algorithm>
+#include <mutex>
 
 #include "common.h"
 
@@ -91,6 +94,43 @@ int check_dtype(int dt, const char* what) {
 }  // namespace xk
 
 using namespace xk;
+
+// ---------------------------------------------------------------------------
+// xk_moe_int4_w4a16_noalloc: the fused INT4 call for callers that cannot
+// allocate. Its scratch is `scratch`, a device array of kNoAllocScratchBytes
+// that every GPU this library runs on holds from module load until the process
+// ends. In host code `scratch` names a host-side stand-in, so its device
+// address is looked up once per device (hipGetSymbolAddress, with that device
+// current) and only that address is handed to kernels. Nothing in the fused
+// pipeline needs the scratch zeroed (align and the GEMM write every element the
+// later kernels read), so no clearing launch is made. Calls that overlap on one
+// GPU share the array and race.
+namespace xk {
+namespace {
+constexpr int64_t kNoAllocScratchBytes = int64_t(64) << 20;
+constexpr int kMaxDevices = 64;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+std::mutex g_scratch_mu;
+void* g_scratch_dev[kMaxDevices] = {};
+
+int noalloc_scratch(void** ptr) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return set_error(XK_ERR_LAUNCH, "int4 noalloc: no current device (%d)", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_dev[dev] == nullptr) {
+    void* p = nullptr;
+    hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      return set_error(XK_ERR_LAUNCH, "int4 noalloc: hipGetSymbolAddress(scratch) on device %d: %s",
+                       dev, hipGetErrorString(e));
+    g_scratch_dev[dev] = p;
+  }
+  *ptr = g_scratch_dev[dev];
+  return XK_OK;
+}
+}  // namespace
+}  // namespace xk
 
 extern "C" {
 
@@ -216,6 +256,32 @@ int xk_moe_int4_w4a16(const void* A, int32_t a_dtype, int64_t M, int64_t K,
   return launch_topk_combine(slot_out, M, top_k, N, topk_w, mul_routed_weight, topk_ids,
                              int(E), expert_map, num_global_experts, out, a_dtype,
                              int(parts), stream);
+}
+
+// ---------------------------------------------------------------------------
+int64_t xk_moe_int4_w4a16_noalloc_max_bytes() { return xk::kNoAllocScratchBytes; }
+
+int xk_moe_int4_w4a16_noalloc(const void* A, int32_t a_dtype, int64_t M, int64_t K,
+                              const int32_t* packed, const uint16_t* scale, int64_t E, int64_t N,
+                              int32_t group_size, const int32_t* topk_ids, const float* topk_w,
+                              int64_t top_k, const int32_t* expert_map,
+                              int32_t num_global_experts, int32_t mul_routed_weight,
+                              int32_t flags, void* out, hipStream_t stream) {
+  clear_error();
+  XK_REQUIRE(M >= 0 && top_k >= 1 && E >= 1 && N >= 1 && K >= 1,
+             "int4 noalloc: bad sizes M=%lld top_k=%lld E=%lld N=%lld K=%lld", (long long)M,
+             (long long)top_k, (long long)E, (long long)N, (long long)K);
+  if (M == 0) return XK_OK;
+  const int64_t need = xk_moe_int4_w4a16_workspace_bytes(M, top_k, E, N, K);
+  XK_REQUIRE(need <= xk::kNoAllocScratchBytes,
+             "int4 noalloc: the call needs %lld B of scratch, above the fixed %lld B "
+             "(use xk_moe_int4_w4a16 with a workspace)",
+             (long long)need, (long long)xk::kNoAllocScratchBytes);
+  void* ws = nullptr;
+  if (int rc = xk::noalloc_scratch(&ws)) return rc;
+  return xk_moe_int4_w4a16(A, a_dtype, M, K, packed, scale, E, N, group_size, topk_ids, topk_w,
+                           top_k, expert_map, num_global_experts, mul_routed_weight, flags, out,
+                           ws, xk::kNoAllocScratchBytes, stream);
 }
 
 int64_t xk_moe_mxfp4_workspace_bytes(int64_t M, int64_t top_k, int64_t E, int64_t hidden,
