@@ -15,7 +15,8 @@ address-stable workspace) and replayed; its time is reported beside the eager
 one as ``ms_per_step_graph`` (``value`` stays the eager rate).
 
     python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--no-cpu] [--fast-dequant]
-    python bench.py --workload {c3-align,c3-reduce,c4,c5,f1-down} [--m M]   (secondary lines)
+    python bench.py --workload {c3-align,c3-reduce,c4,c5,f1-down,topk-softmax} [--m M]
+        (secondary lines)
 """
 from __future__ import annotations
 
@@ -44,7 +45,7 @@ def parse() -> argparse.Namespace:
                     help="exact (n-8)*s contraction instead of the reference's bf16-rounded weights")
     ap.add_argument("--seed", type=int, default=20)
     ap.add_argument("--workload", default="c2",
-                    choices=["c2", "c3-align", "c3-reduce", "c4", "c5", "f1-down"],
+                    choices=["c2", "c3-align", "c3-reduce", "c4", "c5", "f1-down", "topk-softmax"],
                     help="c2 is the headline line; the others time the other BASELINE configs' "
                          "kernels and the layer's down projection (secondary lines, not the "
                          "headline metric)")
@@ -277,6 +278,21 @@ def secondary(a) -> dict:
                 "config": {"workload": "C4 mxfp4 decode", "E_active": e_active},
                 "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
                              "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                             "algorithmic_bytes": nbytes}}
+    if a.workload == "topk-softmax":
+        # the router ahead of the MoE call, at the reference card's measured shape
+        from xkernels_amd import topk_softmax
+
+        M, E, k = 4096, 256, 8
+        logits = torch.randn(M, E, generator=g).to(torch.bfloat16).cuda()
+        ms = _event_time(lambda: topk_softmax(logits, k, backend=hip), a.steps, a.warmup)
+        nbytes = M * E * 2 + M * k * 8
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        return {"metric": "topk_softmax µs at M=4096,E=256,topk=8 bf16 (renormalize)",
+                "value": round(ms * 1e3, 2), "unit": "µs", "higher_is_better": False,
+                "config": {"workload": "topk_softmax router"},
+                "roofline": {"bound": "hbm", "kernel": "topk_softmax_rows", "achieved": round(gbs, 1),
+                             "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
                              "algorithmic_bytes": nbytes}}
     if a.workload == "f1-down":
         # the layer's down projection: N=7168 (hidden), K=2048 (intermediate), E=48

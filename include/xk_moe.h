@@ -50,6 +50,7 @@ extern "C" {
 
 #define XK_DT_BF16 0
 #define XK_DT_FP32 1
+#define XK_DT_FP16 2 /* accepted by xk_moe_topk_softmax only */
 #define XK_DT_NONE (-1) /* "no tensor" for optional weights */
 
 /* int4 flags. Default (0): every dequantised weight is rounded to bf16 before
@@ -175,6 +176,18 @@ int xk_moe_topk_combine(const float* slot_out, int64_t M, int64_t top_k,
                         const int32_t* expert_map, int32_t num_global_experts,
                         void* out, int32_t out_dtype, int32_t nparts,
                         hipStream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * topk_softmax — topk_softmax.py:33-120 (the router that produces topk_ids /
+ * topk_w for the MoE calls). probs = softmax(fp32(gating[m, :])) over all E
+ * experts; the k largest in descending probability, ties broken by ascending
+ * expert id; with renormalize the selected weights are divided by their sum.
+ * gating [M, E] bf16 | fp32 | fp16 contiguous; topk_weights fp32 [M, k],
+ * topk_ids int32 [M, k]. 1 <= k <= E <= 2048.
+ * ------------------------------------------------------------------------- */
+int xk_moe_topk_softmax(const void* gating_output, int32_t dtype, int64_t M, int64_t E,
+                        int64_t topk, int32_t renormalize, float* topk_weights,
+                        int32_t* topk_ids, hipStream_t stream);
 
 /* ---------------------------------------------------------------------------
  * fused_moe_mxfp4 — mxfp4_interface.py:22-100 / mxfp4_reference.py:28-112.

@@ -1,6 +1,6 @@
 """CPU oracle of the quantized fused-MoE path — TEST INFRASTRUCTURE ONLY.
 
-A pure-torch restatement of the xkernels reference backend for the four ops on
+A pure-torch restatement of the xkernels reference backend for the five ops on
 the path. Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s CPU
 baseline may import it, and only as the checker / the timed CPU baseline; the
 ``xkernels_amd`` package never imports it. ``register_reference_backends()``
@@ -15,6 +15,7 @@ Reference behaviour followed (paths in the xkernels checkout):
   moe_sum_reduce_ref         src/xkernels/ops/moe/sum_reduce.py:20-39
   dequant_mxfp4(_weight)     src/xkernels/ops/gather/mxfp4.py:39-68, ops/moe/mxfp4.py:38-56
   moe_mxfp4_ref              src/xkernels/ops/moe/mxfp4_reference.py:28-112
+  topk_softmax_ref           src/xkernels/ops/moe/topk_softmax.py:33-95
 
 Each function is pinned by tests/test_oracle.py against closed forms, brute
 force on tiny inputs, invariants and the independent C restatement
@@ -219,6 +220,24 @@ def moe_mxfp4_ref(A, w13, w13_scale, w2, w2_scale, topk_ids, topk_w, b13=None, b
     return out.to(A.dtype)
 
 
+# ----------------------------------------------------------- topk_softmax ----
+
+def topk_softmax_ref(gating_output: torch.Tensor, topk: int, renormalize: bool = True):
+    """fp32 softmax over all experts, the ``topk`` largest probabilities in
+    descending order with ties to the lower expert id (a stable descending
+    sort), then optional division by their sum (topk_softmax.py:33-95).
+    Returns ``(weights fp32 [M, topk], ids int32 [M, topk])``."""
+    M, E = gating_output.shape
+    if not 1 <= int(topk) <= E:
+        raise ValueError(f"topk must satisfy 1 <= topk <= E (got topk={topk}, E={E})")
+    probs = torch.softmax(gating_output.float(), dim=1)
+    ids = torch.sort(probs, dim=1, descending=True, stable=True).indices[:, : int(topk)]
+    w = probs.gather(1, ids)
+    if renormalize:
+        w = w / w.sum(dim=1, keepdim=True)
+    return w.contiguous(), ids.to(torch.int32).contiguous()
+
+
 # ------------------------------------------------------------ registration ----
 
 # The Op Specs name the reference repository's own oracle functions.
@@ -227,11 +246,12 @@ SPEC_REFERENCES = {
     "xkernels.ops.moe.w4a16:moe_align_block_size_ref": moe_align_block_size_ref,
     "xkernels.ops.moe.sum_reduce:moe_sum_reduce_ref": moe_sum_reduce_ref,
     "xkernels.ops.moe.mxfp4_reference:moe_mxfp4_ref": moe_mxfp4_ref,
+    "xkernels.ops.moe.topk_softmax:topk_softmax_ref": topk_softmax_ref,
 }
 
 
 def register_reference_backends() -> None:
-    """Install the oracle as the REFERENCE backend of the four kernels and as the
+    """Install the oracle as the REFERENCE backend of the five kernels and as the
     resolution of the Op Specs' reference paths (test harness only)."""
     from xkernels_amd._backends import Backend
     from xkernels_amd._dispatch import register
@@ -241,5 +261,6 @@ def register_reference_backends() -> None:
     register("moe_align_block_size", Backend.REFERENCE)(moe_align_block_size_ref)
     register("moe_sum_reduce", Backend.REFERENCE)(moe_sum_reduce_ref)
     register("moe_mxfp4", Backend.REFERENCE)(moe_mxfp4_ref)
+    register("topk_softmax", Backend.REFERENCE)(topk_softmax_ref)
     for path, fn in SPEC_REFERENCES.items():
         bind_reference(path, fn)

@@ -37,7 +37,7 @@ def test_library_exports_every_declared_symbol():
 def test_constants_match_header():
     d = _defines()
     for name in ("XK_OK", "XK_ERR_INVALID", "XK_ERR_WORKSPACE", "XK_ERR_LAUNCH", "XK_DT_BF16",
-                 "XK_DT_FP32", "XK_DT_NONE", "XK_INT4_FAST_DEQUANT"):
+                 "XK_DT_FP32", "XK_DT_FP16", "XK_DT_NONE", "XK_INT4_FAST_DEQUANT"):
         assert getattr(_lib, name) == d[name], name
     # the test-only kernel-choice bits live outside the public header
     internal = (_lib.ROOT_CSRC / "int4_flags.h").read_text()
@@ -179,3 +179,17 @@ def test_mxfp4_rejects_bad_arguments(kw, code):
 def test_call_raises_with_message():
     with pytest.raises(RuntimeError, match="xk_moe_sum_reduce failed"):
         _lib.call("xk_moe_sum_reduce", FAKE, 7, 4, 2, 8, None, 0, 1.0, FAKE, None)
+
+
+@pytest.mark.parametrize("kw", [dict(dt=3), dict(E=0), dict(E=2049, k=8), dict(k=0), dict(k=65),
+                                dict(w=None), dict(ids=None), dict(g=None), dict(M=-1)])
+def test_topk_softmax_rejects_bad_arguments(kw):
+    a = dict(g=FAKE, dt=0, M=4, E=64, k=8, renorm=1, w=FAKE, ids=FAKE, stream=None)
+    a.update(kw)
+    assert _rc("xk_moe_topk_softmax", a["g"], a["dt"], a["M"], a["E"], a["k"], a["renorm"], a["w"],
+               a["ids"], a["stream"]) == _lib.XK_ERR_INVALID
+    assert "topk_softmax" in _lib.last_error()
+
+
+def test_topk_softmax_empty_batch_is_ok():
+    assert _rc("xk_moe_topk_softmax", None, 0, 0, 64, 8, 1, None, None, None) == _lib.XK_OK

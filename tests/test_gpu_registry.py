@@ -8,7 +8,7 @@ from xkernels_amd import find_impl, verify, verify_parity
 
 pytestmark = pytest.mark.gpu
 CARDS = ["moe_int4_w4a16.hip@1.0.0", "moe_align_block_size.hip@1.0.0",
-         "moe_sum_reduce.hip@1.0.0", "moe_mxfp4.hip@1.0.0"]
+         "moe_sum_reduce.hip@1.0.0", "moe_mxfp4.hip@1.0.0", "topk_softmax.hip@1.0.0"]
 
 
 @pytest.mark.parametrize("card", CARDS)
@@ -20,7 +20,7 @@ def test_verify_hip_card(card, dev):
 
 
 @pytest.mark.parametrize("op", ["moe_int4_w4a16@1.0.0", "moe_align_block_size@1.0.0",
-                                "moe_sum_reduce@1.0.0", "moe_mxfp4@1.0.0"])
+                                "moe_sum_reduce@1.0.0", "moe_mxfp4@1.0.0", "topk_softmax@1.0.0"])
 def test_verify_parity_hip_vs_reference(op, dev):
     r = verify_parity(op, archs=["amd_cdna4"])
     assert r["device"] == "cuda"

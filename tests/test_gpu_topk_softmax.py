@@ -1,0 +1,89 @@
+"""topk_softmax on the GPU against the oracle (topk_softmax.py:33-95 upstream).
+
+ids must match exactly, including the ascending-id order of tied
+probabilities (bf16/fp16 logits tie often); weights within the Op Spec's
+per-dtype tolerance. Cases follow the reference's tests/test_topk_softmax.py
+(:88-116) plus the edges of this kernel: E not a multiple of 64, E at its
+2048 limit, k = E, k > 64, rows with many exact ties and with probabilities
+that underflow to 0, and the reference's measured shape (M=4096, E=256, k=8).
+"""
+from __future__ import annotations
+
+import pytest
+import torch
+
+from oracle.torch_ref import topk_softmax_ref
+from xkernels_amd import Backend, topk_softmax
+
+pytestmark = pytest.mark.gpu
+TOL = {torch.float32: (1e-5, 1e-6), torch.bfloat16: (1e-2, 1e-2), torch.float16: (1e-2, 1e-2)}
+DTYPES = [torch.bfloat16, torch.float16, torch.float32]
+
+
+def _check(g, k, renorm):
+    w, ids = topk_softmax(g, k, renormalize=renorm, backend=Backend.HIP)
+    rw, rids = topk_softmax_ref(g, k, renorm)
+    assert w.dtype == torch.float32 and ids.dtype == torch.int32
+    assert w.shape == ids.shape == (g.shape[0], k)
+    bad = (ids != rids).any(dim=1)
+    assert not bad.any(), f"ids differ in {int(bad.sum())} rows; first {int(bad.nonzero()[0])}: " \
+                          f"{ids[bad][0].tolist()} vs {rids[bad][0].tolist()}"
+    rtol, atol = TOL[g.dtype]
+    torch.testing.assert_close(w, rw, rtol=rtol, atol=atol)
+
+
+@pytest.mark.parametrize("M,E,k", [(8, 16, 4), (64, 256, 8), (37, 8, 2), (1, 256, 8), (8, 4, 1)])
+@pytest.mark.parametrize("dt", DTYPES)
+@pytest.mark.parametrize("renorm", [True, False])
+def test_matches_oracle(M, E, k, dt, renorm, dev):
+    g = torch.randn(M, E, generator=torch.Generator(device=dev).manual_seed(M * E + k), device=dev).to(dt)
+    _check(g, k, renorm)
+
+
+@pytest.mark.parametrize("M,E,k", [(33, 65, 7), (5, 2048, 64), (3, 2048, 100), (4, 130, 130),
+                                   (9, 1, 1), (17, 384, 12), (2, 1000, 999)])
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float32])
+def test_edge_shapes(M, E, k, dt, dev):
+    print(f"topk_softmax M={M} E={E} k={k} {dt}", flush=True)
+    g = torch.randn(M, E, generator=torch.Generator(device=dev).manual_seed(E + k), device=dev).to(dt)
+    _check(g, k, True)
+    _check(g, k, False)
+
+
+@pytest.mark.parametrize("dt", DTYPES)
+def test_exact_ties_keep_ascending_ids(dev, dt):
+    """Integer logits in a small range: most experts tie with several others."""
+    g = torch.randint(-3, 4, (64, 256), generator=torch.Generator(device=dev).manual_seed(1),
+                      device=dev).to(dt)
+    _check(g, 16, True)
+    _check(g, 200, False)
+
+
+def test_underflowed_probabilities_tie_at_zero(dev):
+    g = torch.full((4, 96), -500.0, device=dev)
+    g[:, 7] = 0.0
+    g[:, 50] = 1.0
+    g[1, 3] = -80.0
+    _check(g, 12, True)
+    w, ids = topk_softmax(g, 5, renormalize=False, backend=Backend.HIP)
+    assert ids[0].tolist() == [50, 7, 0, 1, 2]
+
+
+def test_reference_measured_shape(dev):
+    g = torch.randn(4096, 256, generator=torch.Generator(device=dev).manual_seed(2), device=dev)
+    _check(g.to(torch.bfloat16), 8, True)
+
+
+def test_rejects_bad_topk_and_cpu(dev):
+    g = torch.randn(4, 8, device=dev)
+    with pytest.raises(ValueError):
+        topk_softmax(g, 0, backend=Backend.HIP)
+    with pytest.raises(ValueError):
+        topk_softmax(g, 9, backend=Backend.HIP)
+    with pytest.raises(RuntimeError):
+        topk_softmax(g.cpu(), 2, backend=Backend.HIP)
+
+
+def test_empty_batch(dev):
+    w, ids = topk_softmax(torch.empty(0, 64, device=dev), 4, backend=Backend.HIP)
+    assert w.shape == ids.shape == (0, 4)

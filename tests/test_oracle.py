@@ -14,7 +14,11 @@ restate its own formula:
 * dequant_mxfp4: e2m1 decoded from its sign / exponent / mantissa bit fields,
   e8m0 special code 0xFF;
 * moe_mxfp4_ref: independent C restatement, single-expert dense recomputation,
-  EP partitions, limit disabled vs huge limit.
+  EP partitions, limit disabled vs huge limit, and a hand-computed answer for
+  the clamp and bias branches (tests/_mxfp4_kat.py);
+* topk_softmax_ref: float64 brute force (sort by (-p, id)) on tiny rows with
+  exact ties, the reference test's tie-break answer, closed forms (equal pair
+  = 1/2 each, underflowed probabilities tie at 0), invariants.
 """
 from __future__ import annotations
 
@@ -308,3 +312,76 @@ def test_mxfp4_ref_known_answer_clamp_and_bias():
     c = c_oracle.mxfp4_moe(x["A"], x["w13"], x["w13_scale"], x["w2"], x["w2_scale"], x["topk_ids"],
                            x["topk_w"], b13=x["b13"], b2=x["b2"], swiglu_limit=x["swiglu_limit"])
     kat.check(c.to(torch.bfloat16))
+
+
+# ----------------------------------------------------------- topk_softmax ----
+
+def _brute_topk_softmax(rows: list[list[float]], k: int, renorm: bool):
+    """Float64 softmax per row, experts ordered by (-probability, id)."""
+    import math
+    ws, ids = [], []
+    for r in rows:
+        m = max(r)
+        ex = [math.exp(x - m) for x in r]
+        s = sum(ex)
+        p = [x / s for x in ex]
+        order = sorted(range(len(r)), key=lambda e: (-p[e], e))[:k]
+        w = [p[e] for e in order]
+        if renorm:
+            t = sum(w)
+            w = [x / t for x in w]
+        ws.append(w)
+        ids.append(order)
+    return torch.tensor(ws, dtype=torch.float64), torch.tensor(ids, dtype=torch.int32)
+
+
+@pytest.mark.parametrize("renorm", [True, False])
+@pytest.mark.parametrize("M,E,k", [(6, 7, 3), (5, 16, 4), (3, 64, 8), (4, 9, 9), (2, 5, 1)])
+def test_topk_softmax_ref_vs_brute_force(M, E, k, renorm):
+    # bf16 logits: distinct values are far apart, equal values tie exactly
+    g = torch.Generator().manual_seed(M * 100 + E)
+    logits = (torch.randn(M, E, generator=g) * 2).to(torch.bfloat16)
+    logits[0, 1] = logits[0, E - 1]  # a forced exact tie in row 0
+    w, ids = R.topk_softmax_ref(logits, k, renorm)
+    bw, bids = _brute_topk_softmax(logits.float().tolist(), k, renorm)
+    assert ids.dtype == torch.int32 and w.dtype == torch.float32
+    assert torch.equal(ids, bids)
+    torch.testing.assert_close(w.double(), bw, rtol=1e-6, atol=1e-7)
+
+
+def test_topk_softmax_ref_known_answers():
+    # the reference's own tie-break case (tests/test_topk_softmax.py:62-74)
+    g = torch.tensor([[0.1, 0.2, 0.7, 0.3, 0.0, 0.7, -1.0]])
+    w, ids = R.topk_softmax_ref(g, 3, renormalize=False)
+    assert ids[0].tolist() == [2, 5, 3]
+    assert w[0, 0].item() == w[0, 1].item()
+    # two equal logits and the rest far below: each of the pair gets 1/2
+    g = torch.tensor([[3.0, -30.0, 3.0, -30.0]])
+    w, ids = R.topk_softmax_ref(g, 2, renormalize=False)
+    assert ids[0].tolist() == [0, 2]
+    torch.testing.assert_close(w, torch.tensor([[0.5, 0.5]]), rtol=1e-6, atol=1e-6)
+    # probabilities that underflow to 0 tie and keep ascending ids
+    g = torch.tensor([[0.0, -200.0, 5.0, -300.0, -250.0]])
+    w, ids = R.topk_softmax_ref(g, 5, renormalize=True)
+    assert ids[0].tolist() == [2, 0, 1, 3, 4]
+    assert w[0, 2:].tolist() == [0.0, 0.0, 0.0]
+    # k = E with renorm is the full softmax, sorted
+    g = torch.tensor([[1.0, 2.0, 0.0]])
+    w, ids = R.topk_softmax_ref(g, 3, renormalize=True)
+    assert ids[0].tolist() == [1, 0, 2]
+    torch.testing.assert_close(w[0], torch.softmax(torch.tensor([2.0, 1.0, 0.0]), 0))
+
+
+def test_topk_softmax_ref_invariants_and_errors():
+    g = torch.randn(32, 48, generator=torch.Generator().manual_seed(4))
+    w, ids = R.topk_softmax_ref(g, 6, renormalize=True)
+    torch.testing.assert_close(w.sum(1), torch.ones(32), rtol=1e-6, atol=1e-6)
+    assert bool((w[:, :-1] >= w[:, 1:]).all())
+    w2, ids2 = R.topk_softmax_ref(g, 6, renormalize=False)
+    assert torch.equal(ids, ids2)
+    torch.testing.assert_close(w2, torch.softmax(g, 1).gather(1, ids2.long()))
+    assert all(len(set(r)) == 6 for r in ids.tolist())
+    with pytest.raises(ValueError):
+        R.topk_softmax_ref(g, 0)
+    with pytest.raises(ValueError):
+        R.topk_softmax_ref(g, 49)

@@ -20,6 +20,7 @@ XK_ERR_WORKSPACE = 2
 XK_ERR_LAUNCH = 3
 XK_DT_BF16 = 0
 XK_DT_FP32 = 1
+XK_DT_FP16 = 2
 XK_DT_NONE = -1
 XK_INT4_FAST_DEQUANT = 1
 # Test-only bits of the int4 flags (csrc/int4_flags.h; not part of the ABI):
@@ -48,6 +49,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [_p, _i32, _i64, _i64, _p, _p, _i64, _i64, _i32, _p, _p, _i64, _p, _i32, _i32, _i32, _p,
          _p, _i64, _p],
     ),
+    "xk_moe_topk_softmax": (ctypes.c_int, [_p, _i32, _i64, _i64, _i64, _i32, _p, _p, _p]),
     "xk_moe_int4_w4a16_noalloc_max_bytes": (_i64, []),
     "xk_moe_int4_w4a16_noalloc": (
         ctypes.c_int,

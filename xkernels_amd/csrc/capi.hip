@@ -51,6 +51,9 @@ int launch_int4_gemm(const void* A, int a_dtype, int64_t M, int64_t K, const int
                      int num_global, const int32_t* sorted_ids, const int32_t* offsets,
                      float* slot_out, int flags, void* workspace, int64_t workspace_bytes,
                      hipStream_t stream);
+int topk_softmax_max_experts();
+int launch_topk_softmax(const void* logits, int dtype, int64_t M, int64_t E, int64_t k,
+                        int renorm, float* w, int32_t* ids, hipStream_t stream);
 int mxfp4_block_size();
 int launch_mxfp4_stage(int stage, const void* A, int a_dtype, const uint8_t* w,
                        const uint8_t* ws, const uint16_t* bias, int64_t E, int64_t K,
@@ -282,6 +285,24 @@ int xk_moe_int4_w4a16_noalloc(const void* A, int32_t a_dtype, int64_t M, int64_t
   return xk_moe_int4_w4a16(A, a_dtype, M, K, packed, scale, E, N, group_size, topk_ids, topk_w,
                            top_k, expert_map, num_global_experts, mul_routed_weight, flags, out,
                            ws, xk::kNoAllocScratchBytes, stream);
+}
+
+int xk_moe_topk_softmax(const void* gating_output, int32_t dtype, int64_t M, int64_t E,
+                        int64_t topk, int32_t renormalize, float* topk_weights,
+                        int32_t* topk_ids, hipStream_t stream) {
+  clear_error();
+  XK_REQUIRE(dtype == XK_DT_BF16 || dtype == XK_DT_FP32 || dtype == XK_DT_FP16,
+             "topk_softmax: dtype code %d is not bf16, fp32 or fp16", dtype);
+  XK_REQUIRE(M >= 0 && E >= 1 && E <= topk_softmax_max_experts(),
+             "topk_softmax: bad sizes M=%lld E=%lld (1 <= E <= %d)", (long long)M, (long long)E,
+             topk_softmax_max_experts());
+  XK_REQUIRE(topk >= 1 && topk <= E, "topk_softmax: topk=%lld outside [1, E=%lld]",
+             (long long)topk, (long long)E);
+  XK_REQUIRE(M * E < (int64_t(1) << 40), "topk_softmax: M*E too large");
+  if (M == 0) return XK_OK;
+  XK_REQUIRE(gating_output && topk_weights && topk_ids, "topk_softmax: null pointer");
+  return launch_topk_softmax(gating_output, dtype, M, E, topk, renormalize != 0, topk_weights,
+                             topk_ids, stream);
 }
 
 int64_t xk_moe_mxfp4_workspace_bytes(int64_t M, int64_t top_k, int64_t E, int64_t hidden,

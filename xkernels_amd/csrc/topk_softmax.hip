@@ -1,0 +1,173 @@
+// The MoE router step: softmax over the expert axis in fp32, top-k selection in
+// descending probability with ties broken by ascending expert id, optional
+// renormalisation of the selected weights (contract of the reference's
+// src/xkernels/ops/moe/topk_softmax.py:33-95 and its Op Spec).
+//
+// One wave64 owns one row at a time. Lane l holds experts l, l+64, l+128, ...
+// (every load instruction of the wave reads one contiguous run of logits), so a
+// row of E experts sits in VPT = ceil(E/64) (rounded to a power of two)
+// registers per lane. Max and sum are wave reductions; each of the k rounds
+// picks the wave-wide best (probability, -id) among the experts not yet taken
+// with one xor-shuffle butterfly, and the lane holding the winner marks it.
+// Selections are staged in LDS so the renormalisation and the [M, k] output
+// writes are contiguous across lanes.
+//
+// HBM bound: M*E logits in, M*k (weight, id) pairs out; no scratch.
+#include <stdint.h>
+
+#include "common.h"
+
+namespace xk {
+namespace {
+
+constexpr int kTsWaves = 4;
+constexpr int kTsThreads = kTsWaves * 64;
+
+template <typename T>
+__device__ __forceinline__ float logit_at(const T* p);
+template <>
+__device__ __forceinline__ float logit_at<uint16_t>(const uint16_t* p) {  // bf16 bits
+  return __uint_as_float(uint32_t(*p) << 16);
+}
+template <>
+__device__ __forceinline__ float logit_at<_Float16>(const _Float16* p) {
+  return float(*p);
+}
+template <>
+__device__ __forceinline__ float logit_at<float>(const float* p) {
+  return *p;
+}
+
+// a ranks before b: larger probability, or equal probability and lower id
+__device__ __forceinline__ bool ranks_before(float a, int ia, float b, int ib) {
+  return a > b || (a == b && ia < ib);
+}
+
+template <typename T, int VPT>
+__global__ void __launch_bounds__(kTsThreads)
+topk_softmax_rows(const T* __restrict__ logits, int64_t M, int E, int k, int renorm,
+                  float* __restrict__ w_out, int32_t* __restrict__ id_out) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char ts_lds[];
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  float* sel_w = reinterpret_cast<float*>(ts_lds) + wave * 2 * k;
+  int32_t* sel_id = reinterpret_cast<int32_t*>(sel_w + k);
+
+  for (int64_t row = int64_t(blockIdx.x) * kTsWaves + wave; row < M;
+       row += int64_t(gridDim.x) * kTsWaves) {
+    const T* g = logits + row * E;
+    float p[VPT];
+    float mx = -__builtin_inff();
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+      const int e = j * 64 + lane;
+      p[j] = e < E ? logit_at<T>(g + e) : -__builtin_inff();
+      mx = fmaxf(mx, p[j]);
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+    float sum = 0.f;
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+      const int e = j * 64 + lane;
+      p[j] = e < E ? expf(p[j] - mx) : 0.f;
+      sum += p[j];
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) sum += __shfl_xor(sum, off);
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+      const int e = j * 64 + lane;
+      p[j] = e < E ? p[j] / sum : -1.f;  // padding never ranks above a real expert
+    }
+
+    uint32_t taken = 0;
+    float picked_sum = 0.f;
+    for (int t = 0; t < k; ++t) {
+      float bv = -2.f;
+      int bid = 0x7fffffff;
+#pragma unroll
+      for (int j = 0; j < VPT; ++j) {
+        const int e = j * 64 + lane;
+        if (!((taken >> j) & 1u) && ranks_before(p[j], e, bv, bid)) {
+          bv = p[j];
+          bid = e;
+        }
+      }
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) {
+        const float ov = __shfl_xor(bv, off);
+        const int oid = __shfl_xor(bid, off);
+        if (ranks_before(ov, oid, bv, bid)) {
+          bv = ov;
+          bid = oid;
+        }
+      }
+      // every lane now holds the same winner (bv, bid)
+      if (lane == (bid & 63)) taken |= 1u << (bid >> 6);
+      if (lane == 0) {
+        sel_w[t] = bv;
+        sel_id[t] = bid;
+      }
+      picked_sum += bv;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    for (int t = lane; t < k; t += 64) {
+      const float v = sel_w[t];
+      w_out[row * k + t] = renorm ? v / picked_sum : v;
+      id_out[row * k + t] = sel_id[t];
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+}
+
+template <typename T, int VPT>
+hipError_t launch_vpt(const void* logits, int64_t M, int E, int k, int renorm, float* w,
+                      int32_t* ids, hipStream_t stream) {
+  const int64_t blocks = (M + kTsWaves - 1) / kTsWaves;
+  const int grid = int(blocks < 65536 ? blocks : 65536);
+  const size_t lds = size_t(kTsWaves) * 2 * k * sizeof(float);
+  hipLaunchKernelGGL((topk_softmax_rows<T, VPT>), dim3(grid), dim3(kTsThreads), lds, stream,
+                     static_cast<const T*>(logits), M, E, k, renorm, w, ids);
+  return hipGetLastError();
+}
+
+template <typename T>
+hipError_t launch_typed(const void* logits, int64_t M, int E, int k, int renorm, float* w,
+                        int32_t* ids, hipStream_t stream) {
+  const int per_lane = (E + 63) / 64;
+  if (per_lane <= 1) return launch_vpt<T, 1>(logits, M, E, k, renorm, w, ids, stream);
+  if (per_lane <= 2) return launch_vpt<T, 2>(logits, M, E, k, renorm, w, ids, stream);
+  if (per_lane <= 4) return launch_vpt<T, 4>(logits, M, E, k, renorm, w, ids, stream);
+  if (per_lane <= 8) return launch_vpt<T, 8>(logits, M, E, k, renorm, w, ids, stream);
+  if (per_lane <= 16) return launch_vpt<T, 16>(logits, M, E, k, renorm, w, ids, stream);
+  return launch_vpt<T, 32>(logits, M, E, k, renorm, w, ids, stream);
+}
+
+}  // namespace
+
+int topk_softmax_max_experts() { return 32 * 64; }
+
+int launch_topk_softmax(const void* logits, int dtype, int64_t M, int64_t E, int64_t k,
+                        int renorm, float* w, int32_t* ids, hipStream_t stream) {
+  hipError_t e;
+  switch (dtype) {
+    case XK_DT_BF16:
+      e = launch_typed<uint16_t>(logits, M, int(E), int(k), renorm, w, ids, stream);
+      break;
+    case XK_DT_FP32:
+      e = launch_typed<float>(logits, M, int(E), int(k), renorm, w, ids, stream);
+      break;
+    default:
+      e = launch_typed<_Float16>(logits, M, int(E), int(k), renorm, w, ids, stream);
+      break;
+  }
+  if (e != hipSuccess) return set_error(XK_ERR_LAUNCH, "topk_softmax launch: %s", hipGetErrorString(e));
+  return XK_OK;
+}
+
+}  // namespace xk

@@ -1,8 +1,8 @@
-"""HIP backend of the four MoE ops: thin wrappers over libxk_moe.so.
+"""HIP backend of the five MoE ops: thin wrappers over libxk_moe.so.
 
 Each callable has the reference backend's exact signature (the kwargs splatted
 by ``verify``; src/xkernels/ops/moe/reference.py:22-33, w4a16.py:53-56,
-sum_reduce.py:20-24, mxfp4_reference.py:28-43), checks device / dtype / shape
+sum_reduce.py:20-24, mxfp4_reference.py:28-43, topk_softmax.py:33-37), checks device / dtype / shape
 on the host, allocates outputs and scratch with torch on the caller's device
 and launches on torch's current stream. Errors from the library surface as
 ``RuntimeError``. CPU tensors are rejected with ``RuntimeError`` (the reference
@@ -19,6 +19,7 @@ from .._dispatch import register
 from .workspace import MoeAlignWorkspace, MoeInt4Workspace, MoeMxfp4Workspace, align_max_pad
 
 _DT = {torch.bfloat16: _lib.XK_DT_BF16, torch.float32: _lib.XK_DT_FP32}
+_ROUTER_DT = {**_DT, torch.float16: _lib.XK_DT_FP16}
 
 
 def _need_gpu(op: str, *tensors: torch.Tensor | None) -> torch.device:
@@ -234,8 +235,32 @@ def moe_mxfp4_hip(A: torch.Tensor, w13: torch.Tensor, w13_scale: torch.Tensor, w
     return out
 
 
+# ------------------------------------------------------------- topk_softmax ----
+
+def topk_softmax_hip(gating_output: torch.Tensor, topk: int,
+                     renormalize: bool = True) -> tuple[torch.Tensor, torch.Tensor]:
+    """``topk_softmax`` on the GPU (contract of topk_softmax.py:33-95)."""
+    dev = _need_gpu("topk_softmax", gating_output)
+    if gating_output.dim() != 2:
+        raise RuntimeError(f"topk_softmax: gating_output must be [M, E], got {tuple(gating_output.shape)}")
+    M, E = gating_output.shape
+    if not (1 <= int(topk) <= E):
+        raise ValueError(f"topk must satisfy 1 <= topk <= E (got topk={topk}, E={E})")
+    try:
+        dt = _ROUTER_DT[gating_output.dtype]
+    except KeyError:
+        raise RuntimeError(f"topk_softmax: unsupported dtype {gating_output.dtype} (bf16, fp16, fp32)") from None
+    g = gating_output.contiguous()
+    k = int(topk)
+    weights = torch.empty((M, k), dtype=torch.float32, device=dev)
+    ids = torch.empty((M, k), dtype=torch.int32, device=dev)
+    _lib.call("xk_moe_topk_softmax", _ptr(g), dt, M, E, k, int(bool(renormalize)), _ptr(weights),
+              _ptr(ids), _stream(dev))
+    return weights, ids
+
+
 def register_all() -> None:
-    """Load the library (raises if absent) and register the four HIP callables."""
+    """Load the library (raises if absent) and register the five HIP callables."""
     lib = _lib.load()
     missing = [n for n in _lib.SIGNATURES if not hasattr(lib, n)]
     if missing:
@@ -244,6 +269,7 @@ def register_all() -> None:
     register("moe_sum_reduce", Backend.HIP)(moe_sum_reduce_hip)
     register("moe_int4_w4a16", Backend.HIP)(moe_int4_w4a16_hip)
     register("moe_mxfp4", Backend.HIP)(moe_mxfp4_hip)
+    register("topk_softmax", Backend.HIP)(topk_softmax_hip)
 
 
 __all__ = [
@@ -251,6 +277,7 @@ __all__ = [
     "moe_sum_reduce_hip",
     "moe_int4_w4a16_hip",
     "moe_mxfp4_hip",
+    "topk_softmax_hip",
     "register_all",
     "MoeAlignWorkspace",
 ]

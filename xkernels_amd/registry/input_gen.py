@@ -2,7 +2,8 @@
 
 Recipes follow the reference's registry/input_gen.py:68-159 (same seeds per
 tensor, same distributions) so the same (point, seed, device) gives the same
-inputs; ``moe_mxfp4`` has no generator upstream and gets one here.
+inputs; ``moe_mxfp4`` has no generator upstream and gets one here. The
+``topk_softmax`` logits are N(0, 1) in the point's dtype (:203-215).
 """
 from __future__ import annotations
 
@@ -70,11 +71,18 @@ def _moe_mxfp4(p: dict[str, Any], seed: int, device: str) -> dict[str, Any]:
             "b13": wts["b13"], "b2": wts["b2"], "swiglu_limit": float(p.get("swiglu_limit", 10.0))}
 
 
+def _topk_softmax(p: dict[str, Any], seed: int, device: str) -> dict[str, Any]:
+    dt = to_torch_dtype(p["dtype"])
+    gating = _randn(device, dt, int(p["M"]), int(p["E"]), seed=seed)
+    return {"gating_output": gating, "topk": int(p["topk"]), "renormalize": bool(p["renormalize"])}
+
+
 _GENERATORS: dict[str, Callable[[dict, int, str], dict[str, Any]]] = {
     "moe_sum_reduce@1.0.0": _moe_sum_reduce,
     "moe_align_block_size@1.0.0": _moe_align_block_size,
     "moe_int4_w4a16@1.0.0": _moe_int4_w4a16,
     "moe_mxfp4@1.0.0": _moe_mxfp4,
+    "topk_softmax@1.0.0": _topk_softmax,
 }
 
 
