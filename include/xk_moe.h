@@ -150,8 +150,12 @@ int xk_moe_int4_w4a16_noalloc(const void* A, int32_t a_dtype, int64_t M, int64_t
  * parts) sums them. The workspace (xk_moe_int4_gemm_workspace_bytes(M, K)
  * bytes, 256-byte aligned) holds the fp16 activations XK_INT4_FAST_DEQUANT
  * prepares; other modes do not touch it and accept NULL. A, packed and scale
- * must be 16-byte aligned for the MFMA kernels. Used by benchmarks to time
- * the GEMM alone. */
+ * must be 16-byte aligned for the MFMA kernels. In the decode regime
+ * (xk_moe_int4_gemm_parts(...) > 1 or M * top_k small against E, at most 4096
+ * routed slots) sorted_token_ids and expert_offsets may both be NULL: the
+ * kernel then routes the slots from topk_ids / expert_map itself (the fused
+ * call does this and skips the align). Used by benchmarks to time the GEMM
+ * alone. */
 int32_t xk_moe_int4_block_size(int64_t M, int64_t top_k, int64_t E);
 int32_t xk_moe_int4_gemm_parts(int64_t M, int64_t top_k, int64_t E, int64_t N, int64_t K,
                                int32_t a_dtype, int32_t group_size, int32_t flags);

@@ -29,8 +29,9 @@ pytestmark = pytest.mark.gpu
 REL = 2.0 ** -20
 
 
-def _gemm_rows(A, packed, scale, ids, flags=0):
-    """fp32 per-slot rows of the grouped GEMM (align with the library's block size)."""
+def _gemm_rows(A, packed, scale, ids, flags=0, self_route=False, emap=None):
+    """fp32 per-slot rows of the grouped GEMM (align with the library's block size,
+    or none: the decode kernel then routes the slots itself)."""
     M, K = A.shape
     E, N, _ = packed.shape
     top_k = ids.shape[1]
@@ -45,7 +46,9 @@ def _gemm_rows(A, packed, scale, ids, flags=0):
     aws = torch.empty(max(1, _lib.query("xk_moe_align_workspace_bytes", numel, E)), dtype=torch.uint8,
                       device=dev)
     s = torch.cuda.current_stream().cuda_stream
-    _lib.call("xk_moe_align_block_size", ids.data_ptr(), numel, E, bs, None, 0, sorted_ids.data_ptr(),
+    ng = 0 if emap is None else emap.numel()
+    ep = None if emap is None else emap.data_ptr()
+    _lib.call("xk_moe_align_block_size", ids.data_ptr(), numel, E, bs, ep, ng, sorted_ids.data_ptr(),
               expert_ids.data_ptr(), num_post.data_ptr(), offsets.data_ptr(), aws.data_ptr(),
               aws.numel(), s)
     parts = _lib.query("xk_moe_int4_gemm_parts", M, top_k, E, N, K, _lib.XK_DT_BF16, 32, flags)
@@ -53,8 +56,9 @@ def _gemm_rows(A, packed, scale, ids, flags=0):
     gws = torch.empty(max(256, _lib.query("xk_moe_int4_gemm_workspace_bytes", M, K)), dtype=torch.uint8,
                       device=dev)
     _lib.call("xk_moe_int4_w4a16_gemm", A.data_ptr(), _lib.XK_DT_BF16, M, K, packed.data_ptr(),
-              scale.data_ptr(), E, N, 32, ids.data_ptr(), top_k, None, 0, sorted_ids.data_ptr(),
-              offsets.data_ptr(), out.data_ptr(), flags, gws.data_ptr(), gws.numel(), s)
+              scale.data_ptr(), E, N, 32, ids.data_ptr(), top_k, ep, ng,
+              None if self_route else sorted_ids.data_ptr(), None if self_route else offsets.data_ptr(),
+              out.data_ptr(), flags, gws.data_ptr(), gws.numel(), s)
     torch.cuda.synchronize()
     return out.sum(0)
 
@@ -117,3 +121,33 @@ def test_fast_mode_is_told_apart():
     rows = _gemm_rows(A, packed, scale, ids, flags=_lib.XK_INT4_FAST_DEQUANT)
     with pytest.raises(AssertionError, match="fp32-summation bound"):
         _bounded_check(A, packed, scale, ids, rows)
+
+
+@pytest.mark.parametrize("M,E,N,K,top_k,routing,ep", [
+    (64, 48, 4096, 7168, 8, "uniform", False),  # C2
+    (192, 16, 512, 1024, 4, "zipf", False),     # several 16-row passes per expert
+    (64, 48, 7168, 2048, 8, "zipf", True),      # expert map: half the experts local
+    (1, 48, 4096, 7168, 8, "uniform", False),
+])
+def test_self_routed_rows_equal_aligned_rows(M, E, N, K, top_k, routing, ep):
+    """Without align outputs the decode kernel routes the slots itself; every
+    written row equals the align-fed kernel's bit for bit (same kernel, same
+    per-row arithmetic), dropped slots stay untouched."""
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    print(f"self-route M={M} E={E} N={N} K={K} k={top_k} {routing} ep={ep}", flush=True)
+    ids = uniform_topk(M, top_k, E, 5) if routing == "uniform" else zipf_topk(M, top_k, E, 1.2, 5)
+    A, packed, scale, ids = _device_inputs(M, E, N, K, ids, 13)
+    emap = None
+    if ep:
+        E_loc = E // 2
+        emap = torch.full((E,), -1, dtype=torch.int32, device="cuda")
+        emap[E_loc:] = torch.arange(E_loc, dtype=torch.int32, device="cuda")
+        packed, scale = packed[E_loc:].contiguous(), scale[E_loc:].contiguous()
+    aligned = _gemm_rows(A, packed, scale, ids, emap=emap)
+    routed = _gemm_rows(A, packed, scale, ids, emap=emap, self_route=True)
+    assert torch.equal(torch.isnan(aligned), torch.isnan(routed))
+    assert torch.equal(torch.nan_to_num(aligned), torch.nan_to_num(routed))
+    if ep:
+        local = (ids.reshape(-1) >= E // 2)
+        assert not torch.isnan(routed[local]).any() and torch.isnan(routed[~local]).all()

@@ -44,6 +44,8 @@ int int4_gemm_parts(int64_t M, int64_t top_k, int64_t E, int64_t N, int64_t K, i
                     int group_size, int flags);
 int int4_block_size();
 bool int4_use_stream(int a_dtype, int group_size, int64_t K);
+bool int4_gemm_self_routes(int64_t M, int64_t top_k, int64_t E, int64_t N, int64_t K, int a_dtype,
+                           int group_size, int flags);
 int64_t int4_gemm_workspace_bytes(int64_t M, int64_t K);
 int launch_int4_gemm(const void* A, int a_dtype, int64_t M, int64_t K, const int32_t* packed,
                      const uint16_t* scale, int64_t E, int64_t N, int group_size,
@@ -240,7 +242,9 @@ int xk_moe_int4_w4a16(const void* A, int32_t a_dtype, int64_t M, int64_t K,
                                               numel * N * 4);
   const int32_t* sorted = nullptr;
   const int32_t* offsets = nullptr;
-  if (int4_use_stream(a_dtype, group_size, K)) {
+  // the decode kernel routes for itself; the other MFMA kernels take the align
+  if (int4_use_stream(a_dtype, group_size, K) &&
+      !int4_gemm_self_routes(M, top_k, E, N, K, a_dtype, group_size, flags)) {
     int rc = launch_align(topk_ids, numel, int(E), int4_block_size(), expert_map,
                           num_global_experts, at<int32_t>(workspace, al.sorted),
                           at<int32_t>(workspace, al.expert_ids),

@@ -88,10 +88,11 @@ bool int4_prefill_ok(int a_dtype, int group_size, int64_t K, int64_t N, int64_t 
 bool int4_ksplit_ok(int64_t K, int64_t N, int64_t E, int64_t numel);
 bool int4_rs_ok(int64_t M, int64_t K, int64_t N, int64_t E);
 int rs_slices(int64_t K);
+bool int4_rs_self_route_ok(int64_t numel);
 int launch_int4_rs(const void* A, int64_t M, int64_t K, const int32_t* packed,
                    const uint16_t* scale, int64_t E, int64_t N, int64_t numel, int64_t top_k,
-                   const int32_t* sorted_ids, const int32_t* offsets, float* slot_out,
-                   hipStream_t stream);
+                   const int32_t* sorted_ids, const int32_t* offsets, const int32_t* topk_ids,
+                   const int32_t* emap, int num_global, float* slot_out, hipStream_t stream);
 int launch_int4_prefill(const void* A, int64_t K, const int32_t* packed, const uint16_t* scale,
                         int64_t E, int64_t N, int64_t numel, int64_t top_k,
                         const int32_t* sorted_ids, const int32_t* offsets, float* slot_out,
@@ -141,6 +142,14 @@ int int4_gemm_parts(int64_t M, int64_t top_k, int64_t E, int64_t N, int64_t K, i
              : 1;
 }
 
+// True when launch_int4_gemm may be called without align outputs (the decode
+// kernel then routes the slots itself).
+bool int4_gemm_self_routes(int64_t M, int64_t top_k, int64_t E, int64_t N, int64_t K, int a_dtype,
+                           int group_size, int flags) {
+  return int4_choose(M, top_k, E, N, K, a_dtype, group_size, flags) == Int4Kernel::kRs &&
+         int4_rs_self_route_ok(M * top_k);
+}
+
 int launch_int4_gemm(const void* A, int a_dtype, int64_t M, int64_t K, const int32_t* packed,
                      const uint16_t* scale, int64_t E, int64_t N, int group_size,
                      const int32_t* topk_ids, int64_t top_k, const int32_t* emap,
@@ -157,8 +166,12 @@ int launch_int4_gemm(const void* A, int a_dtype, int64_t M, int64_t K, const int
   XK_REQUIRE(numel < (int64_t(1) << 30), "int4: M*top_k too large");
   if (numel == 0) return XK_OK;
   const Int4Kernel kern = int4_choose(M, top_k, E, N, K, a_dtype, group_size, flags);
+  // the decode kernel routes for itself when no align outputs are given
+  const bool self_route = kern == Int4Kernel::kRs && sorted_ids == nullptr && offsets == nullptr &&
+                          int4_rs_self_route_ok(numel);
   if (kern != Int4Kernel::kSimple) {
-    XK_REQUIRE(sorted_ids && offsets, "int4: the MFMA kernels need the align outputs");
+    XK_REQUIRE(self_route || (sorted_ids && offsets),
+               "int4: the MFMA kernels need the align outputs");
     XK_REQUIRE(reinterpret_cast<uintptr_t>(A) % 16 == 0 &&
                    reinterpret_cast<uintptr_t>(packed) % 16 == 0 &&
                    reinterpret_cast<uintptr_t>(scale) % 16 == 0,
@@ -170,7 +183,7 @@ int launch_int4_gemm(const void* A, int a_dtype, int64_t M, int64_t K, const int
                                  slot_out, stream);
     case Int4Kernel::kRs:
       return launch_int4_rs(A, M, K, packed, scale, E, N, numel, top_k, sorted_ids, offsets,
-                            slot_out, stream);
+                            topk_ids, emap, num_global, slot_out, stream);
     case Int4Kernel::kKsplit: {
       const int64_t need = int4_gemm_workspace_bytes(M, K);
       if (workspace == nullptr || workspace_bytes < need)

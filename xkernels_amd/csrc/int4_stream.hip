@@ -31,7 +31,12 @@
 //     four groups (one per lane group) and each lane applies its own group's
 //     scale during the dequant;
 //   * dequant: dequant_rne (int4_common.h), bit-identical to the reference's
-//     bf16((n - 8) * s).
+//     bf16((n - 8) * s);
+//   * without align outputs (sorted_ids == offsets == null, at most
+//     kRsMaxSelf routed slots) every workgroup routes for itself: the mapped
+//     expert of every slot goes to LDS with a histogram (LDS atomics), and a
+//     segment's 16 rows are found by one wave's ballot scan of that list. The
+//     rows of an expert then follow ascending slot order, like the align.
 #include "int4_common.h"
 
 #ifndef XK_RS_VARIANT
@@ -44,19 +49,32 @@ int device_cu_count();
 
 namespace {
 
-constexpr int kRsWaves = 8;                 // waves per workgroup (one workgroup per CU)
+#ifndef XK_RS_WAVES
+#define XK_RS_WAVES 8
+#endif
+#ifndef XK_RS_RING
+#define XK_RS_RING 2
+#endif
+#ifndef XK_RS_MAXCP
+#define XK_RS_MAXCP 3
+#endif
+constexpr int kRsWaves = XK_RS_WAVES;       // waves per workgroup (one workgroup per CU)
 constexpr int kRsThreads = kRsWaves * 64;
-constexpr int kRsMaxCp = 3;                 // column pairs per wave per chunk
-constexpr int kRsRing = 2;                  // ring slots: line k + 1 in flight while line k computes
+constexpr int kRsMaxCp = XK_RS_MAXCP;       // column pairs per wave per chunk
+constexpr int kRsRing = XK_RS_RING;         // ring slots: lines k+1 .. k+R-1 in flight while line k computes
 constexpr int kRsLdsA = 112 * 1024;         // bytes of LDS for one activation slice
 constexpr int kRsMaxE = 256;
+constexpr int kRsMaxSelf = 4096;            // routed slots a workgroup can route for itself
 
 struct RsArgs {
   const uint16_t* A;        // [M, K] bf16
   const uint32_t* packed;   // [E, N, K/8]
   const uint16_t* scale;    // [E, N, K/32] bf16
-  const int32_t* sorted_ids;
+  const int32_t* sorted_ids;  // align outputs, or both null: route from topk_ids
   const int32_t* offsets;   // [E+1] padded prefix in slots (multiples of 16)
+  const int32_t* topk_ids;  // [numel] (self-routing only)
+  const int32_t* emap;      // nullable expert map (self-routing only)
+  int num_global;
   float* out;               // [S, numel, N] partial planes
   int K, N, E, numel, top_k;
   int slices;               // S: K slices (16 rows x K / S bf16 fit kRsLdsA)
@@ -108,11 +126,14 @@ template <int N, typename F, int I = 0> __device__ __forceinline__ void static_f
   }
 }
 
-__global__ void __launch_bounds__(kRsThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+__global__ void __launch_bounds__(kRsThreads)
+__attribute__((amdgpu_waves_per_eu(kRsWaves / 4, kRsWaves / 4)))
 int4_stream_rne(RsArgs p) {
   __shared__ __attribute__((aligned(16))) u32x4 a_lds[kRsLdsA / 16];
   __shared__ int pref[kRsMaxE + 1];
   __shared__ int row_slot[16];
+  __shared__ int cnt[kRsMaxE];
+  __shared__ int slot_expert[kRsMaxSelf];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = uniform(tid >> 6);
@@ -124,12 +145,26 @@ int4_stream_rne(RsArgs p) {
   const uint32_t kNibMask = in_vgpr(0x000F000Fu), kNibMaskHi = in_vgpr(0x00F000F0u);
 
   // Items per expert: 16-row passes x slices x column pairs. Prefix by wave
-  // 0 into LDS.
+  // 0 into LDS; the 16-row pass count comes from the align offsets or, when
+  // routing here, from an LDS histogram of the mapped experts.
+  const bool self_route = p.offsets == nullptr;
+  if (self_route) {
+    for (int e = tid; e < E; e += kRsThreads) cnt[e] = 0;
+    __syncthreads();
+    for (int i = tid; i < p.numel; i += kRsThreads) {
+      const int e = map_expert(p.topk_ids[i], p.emap, p.num_global, E);
+      slot_expert[i] = e;
+      if (e >= 0) atomicAdd(&cnt[e], 1);
+    }
+    __syncthreads();
+  }
   if (wave == 0) {
     int run = 0;
     for (int base = 0; base < E; base += 64) {
       const int e = base + lane;
-      int x = e < E ? ((p.offsets[e + 1] - p.offsets[e]) >> 4) * S * ncp : 0;
+      int passes = 0;
+      if (e < E) passes = self_route ? (cnt[e] + 15) >> 4 : (p.offsets[e + 1] - p.offsets[e]) >> 4;
+      int x = passes * S * ncp;
 #pragma unroll
       for (int o = 1; o < 64; o <<= 1) {
         const int y = __shfl_up(x, o);
@@ -157,14 +192,36 @@ int4_stream_rne(RsArgs p) {
   // blk = (line * 2 + h) * 4 + j holds, at lane qq * 16 + r, the 8 values
   // k = s Ks + line * 256 + (4 h + qq) * 32 + 8 j .. + 7 of row r, reordered
   // like the nibble unpack. Rows of pad slots read token 0 (never stored).
-  auto load_segment = [&](int row0, int s) __attribute__((always_inline)) {
+  auto load_segment = [&](int e, int pass, int s) __attribute__((always_inline)) {
     lds_sync();  // every wave is done with the previous segment
-    if (tid < 16) {
-      const int sid = p.sorted_ids[row0 + tid];
-      row_slot[tid] = sid < p.numel ? sid : -1;
+    int sid;
+    if (self_route) {
+      // rows pass*16 .. +15 of expert e: its slots in ascending order
+      if (wave == 0) {
+        const int first = pass * 16;
+        if (lane < 16) row_slot[lane] = -1;
+        int seen = 0;
+        for (int i0 = 0; i0 < p.numel && seen < first + 16; i0 += 64) {
+          const int i = i0 + lane;
+          const bool hit = i < p.numel && slot_expert[i] == e;
+          const uint64_t m = __ballot(hit);
+          const int rank = seen + __popcll(m & ((uint64_t(1) << lane) - 1));
+          if (hit && rank >= first && rank < first + 16) row_slot[rank - first] = i;
+          seen += __popcll(m);
+        }
+      }
+      lds_sync();
+      sid = row_slot[c16];
+    } else {
+      const int row0 = uniform(p.offsets[e] + pass * 16);
+      if (tid < 16) {
+        const int t = p.sorted_ids[row0 + tid];
+        row_slot[tid] = t < p.numel ? t : -1;
+      }
+      const int t = p.sorted_ids[row0 + c16];
+      sid = t < p.numel ? t : -1;
     }
-    const int sid = p.sorted_ids[row0 + c16];
-    const int a_voff = (sid < p.numel ? sid / p.top_k : 0) * K * 2 + q * 64;
+    const int a_voff = (sid >= 0 ? sid / p.top_k : 0) * K * 2 + q * 64;
     for (int blk = wave; blk < nblk; blk += kRsWaves) {
       const int j = blk & 3, h = (blk >> 2) & 1, line = blk >> 3;
       dma_16(ra, &a_lds[blk * 64], a_voff, (s * Ks + line * 256 + 128 * h + 8 * j) * 2);
@@ -317,7 +374,7 @@ int4_stream_rne(RsArgs p) {
     const int cpe = min(ncp, cp0 + (item_end - pos));
     const int seg_id = uniform(pos - cp0);
     if (seg_id != loaded) {
-      load_segment(uniform(p.offsets[e] + pass * 16), s);
+      load_segment(e, pass, s);
       loaded = seg_id;
     }
     for (int c0 = cp0; c0 < cpe; c0 += kRsWaves * kRsMaxCp) {
@@ -347,13 +404,15 @@ bool int4_rs_ok(int64_t M, int64_t K, int64_t N, int64_t E) {
          N * (K / 8) * 4 < (int64_t(1) << 31) && M * K * 2 < (int64_t(1) << 31);
 }
 
+bool int4_rs_self_route_ok(int64_t numel) { return numel <= kRsMaxSelf; }
+
 int launch_int4_rs(const void* A, int64_t M, int64_t K, const int32_t* packed,
                    const uint16_t* scale, int64_t E, int64_t N, int64_t numel, int64_t top_k,
-                   const int32_t* sorted_ids, const int32_t* offsets, float* slot_out,
-                   hipStream_t stream) {
+                   const int32_t* sorted_ids, const int32_t* offsets, const int32_t* topk_ids,
+                   const int32_t* emap, int num_global, float* slot_out, hipStream_t stream) {
   RsArgs a{static_cast<const uint16_t*>(A), reinterpret_cast<const uint32_t*>(packed), scale,
-           sorted_ids, offsets, slot_out, int(K), int(N), int(E), int(numel), int(top_k),
-           rs_slices(K), static_cast<uint32_t>(M * K * 2)};
+           sorted_ids, offsets, topk_ids, emap, num_global, slot_out, int(K), int(N), int(E),
+           int(numel), int(top_k), rs_slices(K), static_cast<uint32_t>(M * K * 2)};
   hipLaunchKernelGGL(int4_stream_rne, dim3(static_cast<unsigned>(device_cu_count())),
                      dim3(kRsThreads), 0, stream, a);
   XK_CHECK_LAUNCH("int4_stream_rne");
