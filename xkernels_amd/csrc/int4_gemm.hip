@@ -86,7 +86,7 @@ bool int4_use_stream(int a_dtype, int group_size, int64_t K) {
 
 bool int4_prefill_ok(int a_dtype, int group_size, int64_t K, int64_t N, int64_t E);
 bool int4_ksplit_ok(int64_t K, int64_t N, int64_t E, int64_t numel);
-bool int4_rs_ok(int64_t M, int64_t K, int64_t N, int64_t E);
+bool int4_rs_ok(int64_t M, int64_t top_k, int64_t K, int64_t N, int64_t E);
 int rs_slices(int64_t K);
 bool int4_rs_self_route_ok(int64_t numel);
 int launch_int4_rs(const void* A, int64_t M, int64_t K, const int32_t* packed,
@@ -122,7 +122,7 @@ Int4Kernel int4_choose(int64_t M, int64_t top_k, int64_t E, int64_t N, int64_t K
   if (!int4_use_stream(a_dtype, group_size, K)) return Int4Kernel::kSimple;
   const int64_t numel = M * top_k;
   const bool tile_ok = int4_prefill_ok(a_dtype, group_size, K, N, E);
-  const bool rs_ok = int4_rs_ok(M, K, N, E);
+  const bool rs_ok = int4_rs_ok(M, top_k, K, N, E);
   bool tile = tile_ok && numel >= kPrefillRowsPerExpert * E;
   if (flags & XK_INT4_TEST_FORCE_TILE) tile = tile_ok;
   if (flags & XK_INT4_TEST_FORCE_STREAM) tile = tile && !rs_ok;

@@ -42,6 +42,9 @@
 #ifndef XK_RS_VARIANT
 #define XK_RS_VARIANT 0  // diagnostic builds only: 2 no MFMA, 3 loads only
 #endif
+#ifndef XK_RS_STORE_POLICY
+#define XK_RS_STORE_POLICY 2  // nt: the partial rows are not re-read by this kernel
+#endif
 
 namespace xk {
 
@@ -124,6 +127,31 @@ template <int N, typename F, int I = 0> __device__ __forceinline__ void static_f
     f(std::integral_constant<int, I>{});
     static_for<N, F, I + 1>(static_cast<F&&>(f));
   }
+}
+
+// 4 x 4 transpose across the four lanes of a quad (lane bits 0-1 = b):
+// afterwards lane b holds element b of every lane of its quad, in lane order.
+// Two butterfly stages (partners lane ^ 1, then lane ^ 2), one DPP move per
+// element pair; value selects keep the vector in registers.
+__device__ __forceinline__ f32x4 quad_transpose(f32x4 e) {
+  const int b = threadIdx.x & 3;
+  auto stage = [&](auto mc, auto ctrl) __attribute__((always_inline)) {
+    constexpr int m = decltype(mc)::value;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (i & m) continue;
+      const bool hi = (b & m) != 0;
+      const float lo_v = e[i], hi_v = e[i + m];
+      const float send = hi ? lo_v : hi_v;
+      const float recv = __int_as_float(__builtin_amdgcn_update_dpp(
+          0, __float_as_int(send), decltype(ctrl)::value, 0xF, 0xF, false));
+      e[i] = hi ? recv : lo_v;
+      e[i + m] = hi ? hi_v : recv;
+    }
+  };
+  stage(std::integral_constant<int, 1>{}, std::integral_constant<int, 0xB1>{});  // quad_perm 1,0,3,2
+  stage(std::integral_constant<int, 2>{}, std::integral_constant<int, 0x4E>{});  // quad_perm 2,3,0,1
+  return e;
 }
 
 __global__ void __launch_bounds__(kRsThreads)
@@ -316,36 +344,53 @@ int4_stream_rne(RsArgs p) {
       }
     };
 
-    // End of a column pair: its partial rows (this slice) to plane s.
-    auto flush = [&](int i) __attribute__((always_inline)) {
-      float* base = p.out + s * plane + (my_lo + i) * 32 + c16;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int slot = row_slot[4 * q + r];
-        if (slot >= 0) {
-          base[static_cast<int64_t>(slot) * N] = acc[0][r];
-          base[static_cast<int64_t>(slot) * N + 16] = acc[1][r];
-        }
+    // Partial rows go to plane s through a buffer resource: a store whose
+    // offset lies past the plane is dropped by the hardware. Every step issues
+    // the same two 16-byte stores (real ones at the end of a column pair, for
+    // the rows of routed slots; out of range otherwise), so the number of
+    // memory operations between a load and its use does not depend on the
+    // path, and the wait before each step's MFMAs never covers a store (the
+    // counter is in issue order).
+    const __amdgpu_buffer_rsrc_t ro = __builtin_amdgcn_make_buffer_rsrc(
+        p.out + s * plane, 0, static_cast<int>(plane * 4), 0x00020000);
+    constexpr uint32_t kDrop = 0x80000000u;
+    const int qb = lane & 3, qa = (lane >> 2) & 3;  // c16 = 4 qa + qb
+
+    // End of a column pair: after a quad transpose lane (qa, qb, q) holds row
+    // 4 q + qb, columns 4 qa .. 4 qa + 3 of each 16-column tile.
+    auto flush_store = [&](bool tend, int i) __attribute__((always_inline)) {
+      f32x4 d0 = acc[0], d1 = acc[1];
+      uint32_t off = kDrop;
+      if (tend) {
+        d0 = quad_transpose(acc[0]);
+        d1 = quad_transpose(acc[1]);
+        const int slot = row_slot[4 * q + qb];
+        if (slot >= 0) off = static_cast<uint32_t>((slot * N + (my_lo + i) * 32 + 4 * qa) * 4);
+        acc[0] = acc[1] = f32x4{0.f, 0.f, 0.f, 0.f};
       }
-      acc[0] = acc[1] = f32x4{0.f, 0.f, 0.f, 0.f};
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, d0), ro, off, 0, XK_RS_STORE_POLICY);
+      // (off + 64 stays out of range for a dropped pair; distinct offsets keep
+      // the compiler from merging the two stores)
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, d1), ro, off + 64, 0,
+                                             XK_RS_STORE_POLICY);
     };
 
     // Ring of kRsRing slots: step k issues the loads of step k + kRsRing - 1
     // into the slot freed by step k - 1, then computes step k.
-    static_for<kRsRing - 1>([&](auto d) {
-      issue(rg[d]);
-      __builtin_amdgcn_sched_barrier(0);
-    });
+    static_for<kRsRing - 1>([&](auto d) { issue(rg[d]); });
+    flush_store(false, 0);  // the two dropped stores every step ends with
     auto step = [&](auto slot) __attribute__((always_inline)) {
       constexpr int nxt = (decltype(slot)::value + kRsRing - 1) % kRsRing;
       issue(rg[nxt]);
-      __builtin_amdgcn_sched_barrier(0);
+      // Dummy steps compute too (after the chunk's last flush, into
+      // accumulators that are never stored): every path then consumes the
+      // slot's registers, so no temporary aliases a load still in flight and
+      // the compiler adds no vmcnt wait that would drain the prefetched lines.
       const bool real = cst < steps;
-      if (real) compute(rg[slot]);
+      compute(rg[slot]);
       const int cl1 = cl + (real ? 1 : 0);
       const bool tend = cl1 == nl;
-      if (tend) flush(ci);
-      __builtin_amdgcn_sched_barrier(0);
+      flush_store(tend, ci);
       cl = tend ? 0 : cl1;
       ci += tend ? 1 : 0;
       ++cst;
@@ -399,9 +444,11 @@ int rs_slices(int64_t K) {
   return 0;
 }
 
-bool int4_rs_ok(int64_t M, int64_t K, int64_t N, int64_t E) {
+bool int4_rs_ok(int64_t M, int64_t top_k, int64_t K, int64_t N, int64_t E) {
+  // the last condition: one fp32 partial plane addressable by a buffer resource
   return K % 256 == 0 && N % 32 == 0 && E <= kRsMaxE && rs_slices(K) > 0 &&
-         N * (K / 8) * 4 < (int64_t(1) << 31) && M * K * 2 < (int64_t(1) << 31);
+         N * (K / 8) * 4 < (int64_t(1) << 31) && M * K * 2 < (int64_t(1) << 31) &&
+         M * top_k * N * 4 < (int64_t(1) << 31);
 }
 
 bool int4_rs_self_route_ok(int64_t numel) { return numel <= kRsMaxSelf; }
