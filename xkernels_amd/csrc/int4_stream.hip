@@ -289,7 +289,11 @@ int4_stream_rne(RsArgs p) {
     auto issue = [&](Slot& sl) __attribute__((always_inline)) {
       const int cp = my_lo + pi;
       const int wo = cp * 32 * KW * 4 + s * (Ks >> 1) + pl * 128;
+#if XK_RS_VARIANT == 6
+      const int so = 0;  // diagnostic: every scale load hits one line
+#else
       const int so = cp * 32 * G * 2 + (s * (Ks >> 5) + pl * 8) * 2;
+#endif
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
 #pragma unroll
