@@ -42,6 +42,9 @@
 #ifndef XK_RS_VARIANT
 #define XK_RS_VARIANT 0  // diagnostic builds only: 2 no MFMA, 3 loads only
 #endif
+#ifndef XK_RS_PAIRED
+#define XK_RS_PAIRED 1  // diagnostic builds: 0 splits (expert, pass, slice, pair) items unpaired
+#endif
 #ifndef XK_RS_STORE_POLICY
 #define XK_RS_STORE_POLICY 2  // nt: the partial rows are not re-read by this kernel
 #endif
@@ -168,6 +171,7 @@ int4_stream_rne(RsArgs p) {
   const int c16 = lane & 15, q = lane >> 4;
   const int K = p.K, N = p.N, E = p.E, G = K >> 5, KW = K >> 3;
   const int S = p.slices, Ks = K / S, nl = Ks >> 8;
+  const bool paired = XK_RS_PAIRED && S > 1 && gridDim.x % (8 * S) == 0;
   const int ncp = N >> 5;            // column pairs per expert
   const int nblk = nl * 8;           // 1 KiB operand blocks of one activation slice
   const uint32_t kNibMask = in_vgpr(0x000F000Fu), kNibMaskHi = in_vgpr(0x00F000F0u);
@@ -192,7 +196,7 @@ int4_stream_rne(RsArgs p) {
       const int e = base + lane;
       int passes = 0;
       if (e < E) passes = self_route ? (cnt[e] + 15) >> 4 : (p.offsets[e + 1] - p.offsets[e]) >> 4;
-      int x = passes * S * ncp;
+      int x = passes * (paired ? 1 : S) * ncp;
 #pragma unroll
       for (int o = 1; o < 64; o <<= 1) {
         const int y = __shfl_up(x, o);
@@ -204,10 +208,20 @@ int4_stream_rne(RsArgs p) {
     if (lane == 0) pref[0] = 0;
   }
   __syncthreads();
+  // Item ranges. Paired (S > 1, grid a multiple of 8 S): the workgroups
+  // b, b + 8, ..., b + 8 (S - 1) run on one XCD (workgroups are dealt to the
+  // 8 XCDs round-robin) and stream slices 0 .. S-1 of the same range of
+  // (expert, pass, column pair) items side by side, so the L2 lines of group
+  // scales that straddle a slice boundary (a column's scale row is K / 16
+  // bytes, not a multiple of 128) are fetched once for both. Otherwise the
+  // items (expert, pass, slice, column pair) are split evenly.
   const int total_items = uniform(pref[E]);
-  const int gsz = gridDim.x, b = blockIdx.x;
-  const int item_beg = static_cast<int>(static_cast<int64_t>(total_items) * b / gsz);
-  const int item_end = static_cast<int>(static_cast<int64_t>(total_items) * (b + 1) / gsz);
+  const int b = blockIdx.x;
+  const int gsz = paired ? static_cast<int>(gridDim.x) / S : static_cast<int>(gridDim.x);
+  const int grp = paired ? (b / (8 * S)) * 8 + (b & 7) : b;
+  const int s_fixed = paired ? (b >> 3) % S : 0;
+  const int item_beg = static_cast<int>(static_cast<int64_t>(total_items) * grp / gsz);
+  const int item_end = static_cast<int>(static_cast<int64_t>(total_items) * (grp + 1) / gsz);
 
   const int w_lane = c16 * KW * 4 + q * 16;  // bytes; + 64 h: group 4 h + q of the line
   const int s_lane = c16 * G * 2;            // bytes: the line's 8 group scales
@@ -418,8 +432,8 @@ int4_stream_rne(RsArgs p) {
     }
     const int e = uniform(lo);
     const int local = pos - pref[e];
-    const int seg = local / ncp, cp0 = local - seg * ncp;  // seg = pass * S + slice
-    const int pass = seg / S, s = seg - pass * S;
+    const int seg = local / ncp, cp0 = local - seg * ncp;  // seg = pass (* S + slice)
+    const int pass = paired ? seg : seg / S, s = paired ? s_fixed : seg - pass * S;
     const int cpe = min(ncp, cp0 + (item_end - pos));
     const int seg_id = uniform(pos - cp0);
     if (seg_id != loaded) {
