@@ -40,7 +40,10 @@ namespace xk {
 namespace {
 
 constexpr int kPBM = 128;              // routed rows per tile
-constexpr int kPBN = 256;              // output columns per tile
+#ifndef XK_PREFILL_BN
+#define XK_PREFILL_BN 256
+#endif
+constexpr int kPBN = XK_PREFILL_BN;    // output columns per tile
 constexpr int kPBK = 128;              // k per pipeline step (4 quantisation groups)
 #ifndef XK_PREFILL_WN
 #define XK_PREFILL_WN 8

@@ -45,6 +45,12 @@
 #ifndef XK_RS_PAIRED
 #define XK_RS_PAIRED 1  // diagnostic builds: 0 splits (expert, pass, slice, pair) items unpaired
 #endif
+#ifndef XK_RS_SPLIT
+#define XK_RS_SPLIT 1
+#endif
+#ifndef XK_RS_LOAD_POLICY
+#define XK_RS_LOAD_POLICY 0  // diagnostic builds: cache policy bits of the weight / scale loads
+#endif
 #ifndef XK_RS_STORE_POLICY
 #define XK_RS_STORE_POLICY 2  // nt: the partial rows are not re-read by this kernel
 #endif
@@ -312,8 +318,9 @@ int4_stream_rne(RsArgs p) {
       for (int c = 0; c < 2; ++c) {
 #pragma unroll
         for (int h = 0; h < 2; ++h)
-          sl.w[c][h] = __builtin_amdgcn_raw_buffer_load_b128(rw, w_lane + 64 * h, wo + c * 16 * KW * 4, 0);
-        sl.s[c] = __builtin_amdgcn_raw_buffer_load_b128(rs, s_lane, so + c * 16 * G * 2, 0);
+          sl.w[c][h] = __builtin_amdgcn_raw_buffer_load_b128(rw, w_lane + 64 * h, wo + c * 16 * KW * 4,
+                                                             XK_RS_LOAD_POLICY);
+        sl.s[c] = __builtin_amdgcn_raw_buffer_load_b128(rs, s_lane, so + c * 16 * G * 2, XK_RS_LOAD_POLICY);
       }
       // advance (value selects keep the cursor in scalar registers)
       const int np = pst + 1;
@@ -423,6 +430,7 @@ int4_stream_rne(RsArgs p) {
   // Walk this workgroup's item range: segments of one (expert, pass, slice),
   // cut into chunks of at most kRsWaves * kRsMaxCp column pairs.
   int loaded = -1;  // first item of the segment whose activations are in LDS
+  int rot = 0;      // first wave to take a remainder pair in the next chunk
   int pos = item_beg;
   while (pos < item_end) {
     int lo = 0, hi = E;  // largest e with pref[e] <= pos
@@ -442,8 +450,19 @@ int4_stream_rne(RsArgs p) {
     }
     for (int c0 = cp0; c0 < cpe; c0 += kRsWaves * kRsMaxCp) {
       const int lc = min(kRsWaves * kRsMaxCp, cpe - c0);
+      // lc / 8 pairs each, the remainder to consecutive waves from a rotating
+      // start: wave w runs on SIMD w % 4, so the extra pairs spread over the
+      // SIMDs and across chunks (XK_RS_SPLIT 0: the plain proportional split)
+#if XK_RS_SPLIT
+      const int base = lc / kRsWaves, rem = lc % kRsWaves;
+      const int r = (wave - rot + kRsWaves) % kRsWaves;
+      const int my_lo = c0 + r * base + min(r, rem);
+      const int cnt = base + (r < rem ? 1 : 0);
+      rot = (rot + rem) % kRsWaves;
+#else
       const int my_lo = c0 + wave * lc / kRsWaves;
       const int cnt = c0 + (wave + 1) * lc / kRsWaves - my_lo;
+#endif
       run_chunk(e, s, my_lo, cnt);
     }
     pos += cpe - cp0;
