@@ -79,6 +79,36 @@ __device__ __forceinline__ bf16x8 dequant_rne(uint32_t w, const RneScale& k, uin
   return __builtin_bit_cast(bf16x8, b);
 }
 
+// dequant_rne with the elements in natural k order n0 .. n7: the same
+// and_or / fma_mix / cvt instructions, with the cvt pairing the fma_mix results
+// of nibbles (2d, 2d + 1) instead of (d, d + 4). Contraction partners then need
+// no permutation.
+__device__ __forceinline__ bf16x8 dequant_rne_nat(uint32_t w, const RneScale& k, uint32_t mlo,
+                                                  uint32_t mhi) {
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  typedef float f2 __attribute__((ext_vector_type(2)));
+  typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+  const uint32_t w8 = w >> 8;
+  // x[d] holds nibbles (d, d + 4) in natural order of d: x0 (n0, n4), x1 (n1, n5),
+  // x2 (n2, n6), x3 (n3, n7)
+  const h2 x[4] = {__builtin_bit_cast(h2, and_or(w, mlo, 0x64006400u)),
+                   __builtin_bit_cast(h2, and_or(w, mhi, 0x54005400u)),
+                   __builtin_bit_cast(h2, and_or(w8, mlo, 0x64006400u)),
+                   __builtin_bit_cast(h2, and_or(w8, mhi, 0x54005400u))};
+  float v[8];
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    const float c = (d & 1) ? k.m72 : k.m1032;
+    v[d] = fmaf(static_cast<float>(x[d][0]), k.s, c);      // nibble d
+    v[d + 4] = fmaf(static_cast<float>(x[d][1]), k.s, c);  // nibble d + 4
+  }
+  u32x4 b;
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    b[e] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f2{v[2 * e], v[2 * e + 1]}), b2));
+  return __builtin_bit_cast(bf16x8, b);
+}
+
 // 8 nibbles -> fp16 in dequant_rne's element order n0 n4 n1 n5 n2 n6 n3 n7:
 // pairs (n0, n4) and (n2, n6) read 1024 + n, pairs (n1, n5) and (n3, n7) read
 // 1024 + 16 n (one v_and_or_b32 per pair, one shift per word). The contraction

@@ -21,8 +21,7 @@
 //     (8 x 2 tiles of v_mfma_f32_16x16x32_bf16, 64 accumulator registers), so
 //     every weight is dequantised by exactly one wave;
 //   * per 128-k step the 128 gathered activation rows are staged in LDS (double
-//     buffered), k-permuted within each 8-group to the order the nibble unpack
-//     yields. gfx950 serves a 16-byte LDS read for 32 lanes at a time from 128
+//     buffered) as they are (the dequant emits natural k order). gfx950 serves a 16-byte LDS read for 32 lanes at a time from 128
 //     banks, so the 32 lanes (16 rows x 2 lane groups) of one read must hit 32
 //     distinct 16-byte bank groups: rows are 288 bytes apart (18 groups) and the
 //     16-byte chunk (lane group q, MFMA j) of a row sits at chunk 4j + q, which
@@ -30,8 +29,8 @@
 //   * lane (c, q) of a wave loads 16 bytes = 32 k of its weight row (quantisation
 //     group q of the step) directly into registers, two steps ahead, and
 //     dequantises each word with the same fp16-magic / fma_mix / RNE sequence as
-//     the decode kernel, which reproduces the reference's bf16-rounded weights
-//     bit for bit.
+//     the decode kernel (dequant_rne_nat: results paired in natural k order),
+//     which reproduces the reference's bf16-rounded weights bit for bit.
 #include <algorithm>
 
 #include "int4_common.h"
@@ -167,13 +166,10 @@ int4_prefill_gemm(PrefillArgs p) {
     auto store_a = [&](int buf, const u32x4 (&ar)[kStPasses]) {
 #pragma unroll
       for (int i = 0; i < kStPasses; ++i) {
-        const uint32_t in[4] = {ar[i][0], ar[i][1], ar[i][2], ar[i][3]};
-        uint32_t o[4];
-        perm8(in, o);
-        // global chunk st_kv = 4 q + j goes to chunk 4 j + q
+        // global chunk st_kv = 4 q + j goes to chunk 4 j + q (natural k order
+        // inside the chunk: the dequant emits natural order)
         *reinterpret_cast<u32x4*>(
-            &a_lds[buf][(st_row + kStRows * i) * kPStride + ((st_kv & 3) * 4 + (st_kv >> 2)) * 8]) =
-            u32x4{o[0], o[1], o[2], o[3]};
+            &a_lds[buf][(st_row + kStRows * i) * kPStride + ((st_kv & 3) * 4 + (st_kv >> 2)) * 8]) = ar[i];
       }
     };
     auto load_w = [&](int s, u32x4 (&w)[kCT], uint32_t (&sv)[kCT]) {
@@ -204,7 +200,7 @@ int4_prefill_gemm(PrefillArgs p) {
               &a_lds[buf][(wm * kRT * 16 + i * 16 + c16) * kPStride + (j * 4 + q) * 8]);
 #pragma unroll
         for (int c = 0; c < kCT; ++c) {
-          const bf16x8 b = dequant_rne(w[c][j], ks[c], kNibMask, kNibMaskHi);
+          const bf16x8 b = dequant_rne_nat(w[c][j], ks[c], kNibMask, kNibMaskHi);
 #pragma unroll
           for (int i = 0; i < kRT; ++i)
             acc[i][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], b, acc[i][c], 0, 0, 0);

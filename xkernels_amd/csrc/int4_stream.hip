@@ -20,8 +20,8 @@
 //     contiguous range holds one or two (expert, pass, slice) segments;
 //   * the segment's activations (16 rows x K / S bf16, 112 KiB) are loaded
 //     once into LDS by direct-to-LDS loads, already in MFMA operand order (a
-//     1 KiB operand is one ds_read_b128 at lane * 16, conflict-free), then
-//     each lane reorders its own 8 values like the nibble unpack;
+//     1 KiB operand is one ds_read_b128 at lane * 16, conflict-free), in
+//     natural k order, which is the order dequant_rne_nat emits;
 //   * each wave streams its column pairs with no barrier: a ring of lines
 //     (4 x 16-byte weight loads and 2 x 16-byte scale loads per 128-byte line
 //     of 32 columns) in flight, one line dequantised and contracted per step;
@@ -30,7 +30,7 @@
 //     column and instruction. Word j of it feeds MFMA j, so an MFMA contracts
 //     four groups (one per lane group) and each lane applies its own group's
 //     scale during the dequant;
-//   * dequant: dequant_rne (int4_common.h), bit-identical to the reference's
+//   * dequant: dequant_rne_nat (int4_common.h), bit-identical to the reference's
 //     bf16((n - 8) * s);
 //   * without align outputs (sorted_ids == offsets == null, at most
 //     kRsMaxSelf routed slots) every workgroup routes for itself: the mapped
@@ -238,8 +238,8 @@ int4_stream_rne(RsArgs p) {
 
   // Activation slice of a segment -> LDS, in operand order: 1 KiB block
   // blk = (line * 2 + h) * 4 + j holds, at lane qq * 16 + r, the 8 values
-  // k = s Ks + line * 256 + (4 h + qq) * 32 + 8 j .. + 7 of row r, reordered
-  // like the nibble unpack. Rows of pad slots read token 0 (never stored).
+  // k = s Ks + line * 256 + (4 h + qq) * 32 + 8 j .. + 7 of row r, in k
+  // order. Rows of pad slots read token 0 (never stored).
   auto load_segment = [&](int e, int pass, int s) __attribute__((always_inline)) {
     lds_sync();  // every wave is done with the previous segment
     int sid;
@@ -275,13 +275,6 @@ int4_stream_rne(RsArgs p) {
       dma_16(ra, &a_lds[blk * 64], a_voff, (s * Ks + line * 256 + 128 * h + 8 * j) * 2);
     }
     XK_WAIT_VMCNT(0);
-    for (int blk = wave; blk < nblk; blk += kRsWaves) {
-      u32x4& x = a_lds[blk * 64 + lane];
-      const u32x4 v = x;
-      uint32_t in[4] = {v[0], v[1], v[2], v[3]}, o[4];
-      perm8(in, o);
-      x = u32x4{o[0], o[1], o[2], o[3]};
-    }
     lds_sync();
   };
 
@@ -350,7 +343,7 @@ int4_stream_rne(RsArgs p) {
 #if XK_RS_VARIANT == 3
             bfrag[c] = __builtin_bit_cast(bf16x8, sl.w[c][h]);
 #else
-            bfrag[c] = dequant_rne(sl.w[c][h][j], ks[c], kNibMask, kNibMaskHi);
+            bfrag[c] = dequant_rne_nat(sl.w[c][h][j], ks[c], kNibMask, kNibMaskHi);
 #endif
           }
 #if XK_RS_VARIANT == 2 || XK_RS_VARIANT == 3
