@@ -73,6 +73,10 @@ namespace {
 constexpr int kRsWaves = XK_RS_WAVES;       // waves per workgroup (one workgroup per CU)
 constexpr int kRsThreads = kRsWaves * 64;
 constexpr int kRsMaxCp = XK_RS_MAXCP;       // column pairs per wave per chunk
+#ifndef XK_RS_KEEP
+#define XK_RS_KEEP 8
+#endif
+constexpr int kRsKeep = XK_RS_KEEP;         // finished column pairs a wave holds before writing
 constexpr int kRsRing = XK_RS_RING;         // ring slots: lines k+1 .. k+R-1 in flight while line k computes
 constexpr int kRsLdsA = 112 * 1024;         // bytes of LDS for one activation slice
 constexpr int kRsMaxE = 256;
@@ -280,6 +284,33 @@ int4_stream_rne(RsArgs p) {
 
   // One chunk: this wave's `cnt` column pairs from `my_lo` of expert e,
   // slice s, each nl lines; results to plane s.
+  // Finished column pairs stay in registers (up to kRsKeep per wave) and are
+  // written after the wave's stream: writes interleaved with the read stream
+  // cost about their own read time again (17.7 MB of partial rows: 17 us at
+  // C2), a burst at the end costs their write time. After a quad transpose
+  // lane (qa, qb, q) holds row 4 q + qb, columns 4 qa .. 4 qa + 3 of each
+  // 16-column tile: two 16-byte stores per kept pair, through a buffer
+  // resource (a dropped row's offset lies past the planes).
+  const __amdgpu_buffer_rsrc_t ro = __builtin_amdgcn_make_buffer_rsrc(
+      p.out, 0, static_cast<int>(plane * 4 * S), 0x00020000);
+  constexpr uint32_t kDrop = 0x80000000u;
+  const int qb = lane & 3, qa = (lane >> 2) & 3;  // c16 = 4 qa + qb
+  f32x4 keep[kRsKeep][2];
+  uint32_t keep_off[kRsKeep];
+  int nkeep = 0;  // wave-uniform
+  auto write_kept = [&]() __attribute__((always_inline)) {
+    static_for<kRsKeep>([&](auto I) {
+      if (decltype(I)::value < nkeep) {
+        const f32x4 d0 = quad_transpose(keep[I][0]), d1 = quad_transpose(keep[I][1]);
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, d0), ro, keep_off[I], 0,
+                                               XK_RS_STORE_POLICY);
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, d1), ro, keep_off[I] + 64, 0,
+                                               XK_RS_STORE_POLICY);
+      }
+    });
+    nkeep = 0;
+  };
+
   auto run_chunk = [&](int e, int s, int my_lo, int cnt) __attribute__((always_inline)) {
     if (cnt == 0) return;
     const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
@@ -362,53 +393,39 @@ int4_stream_rne(RsArgs p) {
       }
     };
 
-    // Partial rows go to plane s through a buffer resource: a store whose
-    // offset lies past the plane is dropped by the hardware. Every step issues
-    // the same two 16-byte stores (real ones at the end of a column pair, for
-    // the rows of routed slots; out of range otherwise), so the number of
-    // memory operations between a load and its use does not depend on the
-    // path, and the wait before each step's MFMAs never covers a store (the
-    // counter is in issue order).
-    const __amdgpu_buffer_rsrc_t ro = __builtin_amdgcn_make_buffer_rsrc(
-        p.out + s * plane, 0, static_cast<int>(plane * 4), 0x00020000);
-    constexpr uint32_t kDrop = 0x80000000u;
-    const int qb = lane & 3, qa = (lane >> 2) & 3;  // c16 = 4 qa + qb
-
-    // End of a column pair: after a quad transpose lane (qa, qb, q) holds row
-    // 4 q + qb, columns 4 qa .. 4 qa + 3 of each 16-column tile.
-    auto flush_store = [&](bool tend, int i) __attribute__((always_inline)) {
-      f32x4 d0 = acc[0], d1 = acc[1];
-      uint32_t off = kDrop;
-      if (tend) {
-        d0 = quad_transpose(acc[0]);
-        d1 = quad_transpose(acc[1]);
-        const int slot = row_slot[4 * q + qb];
-        if (slot >= 0) off = static_cast<uint32_t>((slot * N + (my_lo + i) * 32 + 4 * qa) * 4);
-        acc[0] = acc[1] = f32x4{0.f, 0.f, 0.f, 0.f};
-      }
-      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, d0), ro, off, 0, XK_RS_STORE_POLICY);
-      // (off + 64 stays out of range for a dropped pair; distinct offsets keep
-      // the compiler from merging the two stores)
-      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, d1), ro, off + 64, 0,
-                                             XK_RS_STORE_POLICY);
+    // End of a column pair: its partial rows (this slice) join the kept ones.
+    auto finish_pair = [&](int i) __attribute__((always_inline)) {
+      const int slot = row_slot[4 * q + qb];
+      const uint32_t off =
+          slot >= 0 ? static_cast<uint32_t>(((s * p.numel + slot) * N + (my_lo + i) * 32 + 4 * qa) * 4)
+                    : kDrop;
+      static_for<kRsKeep>([&](auto I) {
+        if (nkeep == decltype(I)::value) {
+          keep[I][0] = acc[0];
+          keep[I][1] = acc[1];
+          keep_off[I] = off;
+        }
+      });
+      ++nkeep;
+      acc[0] = acc[1] = f32x4{0.f, 0.f, 0.f, 0.f};
+      if (nkeep == kRsKeep) write_kept();  // only shapes with many pairs per wave
     };
 
     // Ring of kRsRing slots: step k issues the loads of step k + kRsRing - 1
     // into the slot freed by step k - 1, then computes step k.
     static_for<kRsRing - 1>([&](auto d) { issue(rg[d]); });
-    flush_store(false, 0);  // the two dropped stores every step ends with
     auto step = [&](auto slot) __attribute__((always_inline)) {
       constexpr int nxt = (decltype(slot)::value + kRsRing - 1) % kRsRing;
       issue(rg[nxt]);
-      // Dummy steps compute too (after the chunk's last flush, into
-      // accumulators that are never stored): every path then consumes the
+      // Dummy steps compute too (after the chunk's last pair, into
+      // accumulators that are never kept): every path then consumes the
       // slot's registers, so no temporary aliases a load still in flight and
       // the compiler adds no vmcnt wait that would drain the prefetched lines.
       const bool real = cst < steps;
       compute(rg[slot]);
       const int cl1 = cl + (real ? 1 : 0);
       const bool tend = cl1 == nl;
-      flush_store(tend, ci);
+      if (tend) finish_pair(ci);
       cl = tend ? 0 : cl1;
       ci += tend ? 1 : 0;
       ++cst;
@@ -460,6 +477,7 @@ int4_stream_rne(RsArgs p) {
     }
     pos += cpe - cp0;
   }
+  write_kept();
 }
 
 }  // namespace
@@ -475,10 +493,10 @@ int rs_slices(int64_t K) {
 }
 
 bool int4_rs_ok(int64_t M, int64_t top_k, int64_t K, int64_t N, int64_t E) {
-  // the last condition: one fp32 partial plane addressable by a buffer resource
+  // the last condition: the fp32 partial planes addressable by one buffer resource
   return K % 256 == 0 && N % 32 == 0 && E <= kRsMaxE && rs_slices(K) > 0 &&
          N * (K / 8) * 4 < (int64_t(1) << 31) && M * K * 2 < (int64_t(1) << 31) &&
-         M * top_k * N * 4 < (int64_t(1) << 31);
+         M * top_k * N * 4 * rs_slices(K) < (int64_t(1) << 31);
 }
 
 bool int4_rs_self_route_ok(int64_t numel) { return numel <= kRsMaxSelf; }
