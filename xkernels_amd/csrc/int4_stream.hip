@@ -74,7 +74,7 @@ constexpr int kRsWaves = XK_RS_WAVES;       // waves per workgroup (one workgrou
 constexpr int kRsThreads = kRsWaves * 64;
 constexpr int kRsMaxCp = XK_RS_MAXCP;       // column pairs per wave per chunk
 #ifndef XK_RS_KEEP
-#define XK_RS_KEEP 8
+#define XK_RS_KEEP 9
 #endif
 constexpr int kRsKeep = XK_RS_KEEP;         // finished column pairs a wave holds before writing
 constexpr int kRsRing = XK_RS_RING;         // ring slots: lines k+1 .. k+R-1 in flight while line k computes
@@ -313,6 +313,9 @@ int4_stream_rne(RsArgs p) {
 
   auto run_chunk = [&](int e, int s, int my_lo, int cnt) __attribute__((always_inline)) {
     if (cnt == 0) return;
+    // a chunk adds at most kRsMaxCp pairs: room is made before its stream
+    // starts, so the step loop below never stores
+    if (nkeep > kRsKeep - kRsMaxCp) write_kept();
     const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint32_t*>(p.packed + static_cast<int64_t>(e) * N * KW), 0, N * KW * 4, 0x00020000);
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
@@ -333,11 +336,7 @@ int4_stream_rne(RsArgs p) {
     auto issue = [&](Slot& sl) __attribute__((always_inline)) {
       const int cp = my_lo + pi;
       const int wo = cp * 32 * KW * 4 + s * (Ks >> 1) + pl * 128;
-#if XK_RS_VARIANT == 6
-      const int so = 0;  // diagnostic: every scale load hits one line
-#else
       const int so = cp * 32 * G * 2 + (s * (Ks >> 5) + pl * 8) * 2;
-#endif
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
 #pragma unroll
@@ -408,12 +407,16 @@ int4_stream_rne(RsArgs p) {
       });
       ++nkeep;
       acc[0] = acc[1] = f32x4{0.f, 0.f, 0.f, 0.f};
-      if (nkeep == kRsKeep) write_kept();  // only shapes with many pairs per wave
     };
 
     // Ring of kRsRing slots: step k issues the loads of step k + kRsRing - 1
     // into the slot freed by step k - 1, then computes step k.
-    static_for<kRsRing - 1>([&](auto d) { issue(rg[d]); });
+    // (the barriers keep the prologue's slots in issue order: the loop waits
+    // for slot 0 first, and a reordered prologue would make it wait for all)
+    static_for<kRsRing - 1>([&](auto d) {
+      issue(rg[d]);
+      __builtin_amdgcn_sched_barrier(0);
+    });
     auto step = [&](auto slot) __attribute__((always_inline)) {
       constexpr int nxt = (decltype(slot)::value + kRsRing - 1) % kRsRing;
       issue(rg[nxt]);
