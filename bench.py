@@ -75,6 +75,26 @@ def make_inputs(seed: int, M: int = 64, E: int = 48, N: int = 4096, K: int = 716
     return dict(M=M, E=E, N=N, K=K, top_k=top_k, A=A, packed=packed, scale=scale, ids=ids, w=w)
 
 
+WARM_SECONDS = 0.15
+
+
+def warm(fn, steps: int) -> None:
+    """Untimed warmup: ``steps`` calls, then more until WARM_SECONDS of the same
+    work have run. From idle the GPU takes ~40 ms of load to reach its
+    sustained clock (a C2 step measures ~200-220 us in its first 10 ms and
+    ~179 us from ~40 ms on), so a fixed small step count would time the ramp."""
+    import torch
+
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        fn()
+    torch.cuda.synchronize()
+    while time.perf_counter() - t0 < WARM_SECONDS:
+        for _ in range(20):
+            fn()
+        torch.cuda.synchronize()
+
+
 def time_gemm_kernel(c, flags: int, iters: int) -> float:
     """Average duration (ms) of one grouped-GEMM launch, HIP events on its stream."""
     import torch
@@ -106,9 +126,7 @@ def time_gemm_kernel(c, flags: int, iters: int) -> float:
                   top_k, None, 0, sorted_ids.data_ptr(), offsets.data_ptr(), slot_out.data_ptr(),
                   flags, gws.data_ptr(), gws.numel(), s)
 
-    for _ in range(10):
-        launch()
-    torch.cuda.synchronize()
+    warm(launch, 10)
     starts = [torch.cuda.Event(enable_timing=True) for _ in range(iters)]
     ends = [torch.cuda.Event(enable_timing=True) for _ in range(iters)]
     for i in range(iters):
@@ -201,9 +219,7 @@ def _event_time(fn, steps: int, warmup: int) -> float:
     stream the library launches on)."""
     import torch
 
-    for _ in range(warmup):
-        fn()
-    torch.cuda.synchronize()
+    warm(fn, warmup)
     stream = torch.cuda.current_stream()
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     ev0.record(stream)
@@ -400,9 +416,7 @@ def main() -> int:
     if a.profile_only and a.gemm_only:
         time_gemm_kernel(c, flags, a.steps)
         return 0
-    for _ in range(a.warmup):
-        step()
-    torch.cuda.synchronize()
+    warm(step, a.warmup)
     t0 = time.perf_counter()
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     ev0.record()
@@ -439,7 +453,8 @@ def main() -> int:
                                "uniform routing, softmax weights",
                    "E_active": e_active, "weight_scale_bytes": weight_bytes,
                    "dequant": "bf16-rounded (reference)" if exact else "exact fp32 (fast)",
-                   "wall_s_timed_region": round(wall, 4)},
+                   "wall_s_timed_region": round(wall, 4),
+                   "warm_s_before_timing": WARM_SECONDS},
         "roofline": {"bound": "hbm",
                      "kernel": KERNEL[exact],
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",

@@ -23,8 +23,14 @@
 //     1 KiB operand is one ds_read_b128 at lane * 16, conflict-free), in
 //     natural k order, which is the order dequant_rne_nat emits;
 //   * each wave streams its column pairs with no barrier: a ring of lines
-//     (4 x 16-byte weight loads and 2 x 16-byte scale loads per 128-byte line
-//     of 32 columns) in flight, one line dequantised and contracted per step;
+//     (4 x 16-byte weight loads per 128-byte line of 32 columns) in flight,
+//     one line dequantised and contracted per step;
+//   * group scales come in 4-line blocks: on a block's first line, two loads
+//     read 64 contiguous bytes of every column (lane (c, q): line + q), the
+//     wave parks them in a private 2 KiB LDS area and each step reads its own
+//     line there. A scale load per line instead (16 columns x 16 bytes per
+//     instruction, every step) costs ~10 us more at the headline shape: the
+//     per-instruction spread over 16 columns, not the bytes, is what counts;
 //   * lane (c, q) of a load reads bytes 64 h + 16 q of column c's line: the
 //     whole quantisation group 4 h + q, one contiguous 64-byte half line per
 //     column and instruction. Word j of it feeds MFMA j, so an MFMA contracts
@@ -175,6 +181,7 @@ int4_stream_rne(RsArgs p) {
   __shared__ int row_slot[16];
   __shared__ int cnt[kRsMaxE];
   __shared__ int slot_expert[kRsMaxSelf];
+  __shared__ u32x4 sc_lds[kRsWaves][2][64];  // per wave: a 4-line block of group scales
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = uniform(tid >> 6);
@@ -330,20 +337,25 @@ int4_stream_rne(RsArgs p) {
 
     struct Slot {
       u32x4 w[2][2];  // weights: [column tile][group 4 h + q]
-      u32x4 s[2];     // the line's 8 group scales: [column tile]
+      u32x4 s[2];     // block-start steps: group scales of lines + q [column tile]
     };
     Slot rg[kRsRing];
     auto issue = [&](Slot& sl) __attribute__((always_inline)) {
       const int cp = my_lo + pi;
       const int wo = cp * 32 * KW * 4 + s * (Ks >> 1) + pl * 128;
       const int so = cp * 32 * G * 2 + (s * (Ks >> 5) + pl * 8) * 2;
+      // scales: only on the first line of each 4-line block, where lane
+      // (c16, q) loads line pl + q's 16 bytes (64 contiguous bytes per column)
+      const bool blk = (pl & 3) == 0 && pst < steps;
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
 #pragma unroll
         for (int h = 0; h < 2; ++h)
           sl.w[c][h] = __builtin_amdgcn_raw_buffer_load_b128(rw, w_lane + 64 * h, wo + c * 16 * KW * 4,
                                                              XK_RS_LOAD_POLICY);
-        sl.s[c] = __builtin_amdgcn_raw_buffer_load_b128(rs, s_lane, so + c * 16 * G * 2, XK_RS_LOAD_POLICY);
+        if (blk)
+          sl.s[c] = __builtin_amdgcn_raw_buffer_load_b128(rs, s_lane + 16 * q, so + c * 16 * G * 2,
+                                                          XK_RS_LOAD_POLICY);
       }
       // advance (value selects keep the cursor in scalar registers)
       const int np = pst + 1;
@@ -359,12 +371,21 @@ int4_stream_rne(RsArgs p) {
 
     auto compute = [&](const Slot& sl) __attribute__((always_inline)) {
       const int lbase = cl * (8 * 64) + lane;
+      // block start: the loaded scales go to this wave's LDS area (line q of
+      // the block at 16 q + c16), then every step reads its own line there
+      u32x4 sv[2];
+      if ((cl & 3) == 0) {
+#pragma unroll
+        for (int c = 0; c < 2; ++c) sc_lds[wave][c][lane] = sl.s[c];
+      }
+#pragma unroll
+      for (int c = 0; c < 2; ++c) sv[c] = sc_lds[wave][c][(cl & 3) * 16 + c16];
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         RneScale ks[2];
 #pragma unroll
         for (int c = 0; c < 2; ++c)  // bf16 scale of group 4 h + q -> fp32 (one v_perm_b32)
-          ks[c] = rne_scale(__uint_as_float(__builtin_amdgcn_perm(sl.s[c][2 * h + 1], sl.s[c][2 * h], s_sel)));
+          ks[c] = rne_scale(__uint_as_float(__builtin_amdgcn_perm(sv[c][2 * h + 1], sv[c][2 * h], s_sel)));
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           bf16x8 bfrag[2];
