@@ -39,6 +39,8 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--warm-seconds", type=float, default=WARM_SECONDS,
+                    help="minimum untimed warm work before each timed region (counter passes use 0)")
     ap.add_argument("--gemm-iters", type=int, default=100)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--fast-dequant", action="store_true",
@@ -76,6 +78,7 @@ def make_inputs(seed: int, M: int = 64, E: int = 48, N: int = 4096, K: int = 716
 
 
 WARM_SECONDS = 0.15
+_warm_seconds = WARM_SECONDS
 
 
 def warm(fn, steps: int) -> None:
@@ -89,7 +92,7 @@ def warm(fn, steps: int) -> None:
     for _ in range(steps):
         fn()
     torch.cuda.synchronize()
-    while time.perf_counter() - t0 < WARM_SECONDS:
+    while time.perf_counter() - t0 < _warm_seconds:
         for _ in range(20):
             fn()
         torch.cuda.synchronize()
@@ -385,6 +388,8 @@ def _cpu_model() -> str:
 
 def main() -> int:
     a = parse()
+    global _warm_seconds
+    _warm_seconds = a.warm_seconds
     if a.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only; run with --gpus 1 "
                                    "(multi-GPU expert parallelism is a design note, not a bench line)"}))
@@ -454,7 +459,7 @@ def main() -> int:
                    "E_active": e_active, "weight_scale_bytes": weight_bytes,
                    "dequant": "bf16-rounded (reference)" if exact else "exact fp32 (fast)",
                    "wall_s_timed_region": round(wall, 4),
-                   "warm_s_before_timing": WARM_SECONDS},
+                   "warm_s_before_timing": a.warm_seconds},
         "roofline": {"bound": "hbm",
                      "kernel": KERNEL[exact],
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",

@@ -25,12 +25,14 @@
 //   * each wave streams its column pairs with no barrier: a ring of lines
 //     (4 x 16-byte weight loads per 128-byte line of 32 columns) in flight,
 //     one line dequantised and contracted per step;
-//   * group scales come in 4-line blocks: on a block's first line, two loads
-//     read 64 contiguous bytes of every column (lane (c, q): line + q), the
-//     wave parks them in a private 2 KiB LDS area and each step reads its own
-//     line there. A scale load per line instead (16 columns x 16 bytes per
-//     instruction, every step) costs ~10 us more at the headline shape: the
-//     per-instruction spread over 16 columns, not the bytes, is what counts;
+//   * group scales come in 8-line blocks: on a block's first line, four loads
+//     read 128 contiguous bytes of every column (lane (c, q): lines + q and
+//     + q + 4), the wave parks them in a private 4 KiB LDS area and each step
+//     reads its own line there. A scale load per line instead (16 columns x
+//     16 bytes per instruction, every step) costs ~12 us more at the headline
+//     shape: the per-instruction spread over 16 columns, not the bytes, is
+//     what counts; 8 rather than 4 lines fetch each 128-byte line of scales
+//     once instead of twice (L2 evicts it between the two halves);
 //   * lane (c, q) of a load reads bytes 64 h + 16 q of column c's line: the
 //     whole quantisation group 4 h + q, one contiguous 64-byte half line per
 //     column and instruction. Word j of it feeds MFMA j, so an MFMA contracts
@@ -83,6 +85,11 @@ constexpr int kRsMaxCp = XK_RS_MAXCP;       // column pairs per wave per chunk
 #define XK_RS_KEEP 9
 #endif
 constexpr int kRsKeep = XK_RS_KEEP;         // finished column pairs a wave holds before writing
+#ifndef XK_RS_SCLINES
+#define XK_RS_SCLINES 8
+#endif
+constexpr int kRsScLines = XK_RS_SCLINES;   // lines per block of group scales (4 or 8)
+constexpr int kRsScLoads = kRsScLines / 4;  // 16-byte scale loads per lane and column tile
 constexpr int kRsRing = XK_RS_RING;         // ring slots: lines k+1 .. k+R-1 in flight while line k computes
 constexpr int kRsLdsA = 112 * 1024;         // bytes of LDS for one activation slice
 constexpr int kRsMaxE = 256;
@@ -180,8 +187,8 @@ int4_stream_rne(RsArgs p) {
   __shared__ int pref[kRsMaxE + 1];
   __shared__ int row_slot[16];
   __shared__ int cnt[kRsMaxE];
-  __shared__ int slot_expert[kRsMaxSelf];
-  __shared__ u32x4 sc_lds[kRsWaves][2][64];  // per wave: a 4-line block of group scales
+  __shared__ int16_t slot_expert[kRsMaxSelf];
+  __shared__ u32x4 sc_lds[kRsWaves][2][kRsScLines * 16];  // per wave: a block of group scales
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = uniform(tid >> 6);
@@ -337,25 +344,30 @@ int4_stream_rne(RsArgs p) {
 
     struct Slot {
       u32x4 w[2][2];  // weights: [column tile][group 4 h + q]
-      u32x4 s[2];     // block-start steps: group scales of lines + q [column tile]
+      u32x4 s[2][kRsScLoads];  // block-start steps: scales of lines + q + 4 i [column tile][i]
     };
     Slot rg[kRsRing];
     auto issue = [&](Slot& sl) __attribute__((always_inline)) {
       const int cp = my_lo + pi;
       const int wo = cp * 32 * KW * 4 + s * (Ks >> 1) + pl * 128;
       const int so = cp * 32 * G * 2 + (s * (Ks >> 5) + pl * 8) * 2;
-      // scales: only on the first line of each 4-line block, where lane
-      // (c16, q) loads line pl + q's 16 bytes (64 contiguous bytes per column)
-      const bool blk = (pl & 3) == 0 && pst < steps;
+      // scales: only on the first line of each block, where lane (c16, q)
+      // loads the 16 bytes of lines pl + q + 4 i (16 contiguous bytes per
+      // column and line of the block)
+      const bool blk = (pl & (kRsScLines - 1)) == 0 && pst < steps;
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
 #pragma unroll
         for (int h = 0; h < 2; ++h)
           sl.w[c][h] = __builtin_amdgcn_raw_buffer_load_b128(rw, w_lane + 64 * h, wo + c * 16 * KW * 4,
                                                              XK_RS_LOAD_POLICY);
-        if (blk)
-          sl.s[c] = __builtin_amdgcn_raw_buffer_load_b128(rs, s_lane + 16 * q, so + c * 16 * G * 2,
-                                                          XK_RS_LOAD_POLICY);
+        if (blk) {  // lanes past the slice's last line read nothing (offset past the buffer)
+#pragma unroll
+          for (int i = 0; i < kRsScLoads; ++i)
+            sl.s[c][i] = __builtin_amdgcn_raw_buffer_load_b128(
+                rs, pl + q + 4 * i < nl ? s_lane + 16 * (q + 4 * i) : (1 << 30), so + c * 16 * G * 2,
+                XK_RS_LOAD_POLICY);
+        }
       }
       // advance (value selects keep the cursor in scalar registers)
       const int np = pst + 1;
@@ -371,15 +383,17 @@ int4_stream_rne(RsArgs p) {
 
     auto compute = [&](const Slot& sl) __attribute__((always_inline)) {
       const int lbase = cl * (8 * 64) + lane;
-      // block start: the loaded scales go to this wave's LDS area (line q of
-      // the block at 16 q + c16), then every step reads its own line there
+      // block start: the loaded scales go to this wave's LDS area (line L of
+      // the block at 16 L + c16), then every step reads its own line there
       u32x4 sv[2];
-      if ((cl & 3) == 0) {
+      if ((cl & (kRsScLines - 1)) == 0) {
 #pragma unroll
-        for (int c = 0; c < 2; ++c) sc_lds[wave][c][lane] = sl.s[c];
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+          for (int i = 0; i < kRsScLoads; ++i) sc_lds[wave][c][i * 64 + lane] = sl.s[c][i];
       }
 #pragma unroll
-      for (int c = 0; c < 2; ++c) sv[c] = sc_lds[wave][c][(cl & 3) * 16 + c16];
+      for (int c = 0; c < 2; ++c) sv[c] = sc_lds[wave][c][(cl & (kRsScLines - 1)) * 16 + c16];
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         RneScale ks[2];
