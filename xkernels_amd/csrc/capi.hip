@@ -39,7 +39,8 @@ int launch_sum_reduce(const void* y, int y_dtype, int64_t M, int64_t top_k, int6
 int launch_topk_combine(const float* slot_out, int64_t M, int64_t top_k, int64_t N,
                         const float* topk_w, int mul_routed_weight, const int32_t* topk_ids,
                         int num_local, const int32_t* emap, int num_global, void* out,
-                        int out_dtype, int nparts, hipStream_t stream);
+                        int out_dtype, int nparts, hipStream_t stream,
+                        const uint16_t* post_bias = nullptr, int post_round = 0);
 int int4_gemm_parts(int64_t M, int64_t top_k, int64_t E, int64_t N, int64_t K, int a_dtype,
                     int group_size, int flags);
 int int4_block_size();
@@ -62,6 +63,16 @@ int launch_mxfp4_stage(int stage, const void* A, int a_dtype, const uint8_t* w,
                        int64_t rows, int64_t ncols, const int32_t* sorted_ids,
                        const int32_t* offsets, int64_t numel, int64_t top_k, float limit,
                        uint16_t* act, float* slot_out, hipStream_t stream);
+int mxfp4_rs_slices(int64_t K, int64_t N, int64_t numel, int64_t E);
+bool mxfp4_rs_ok(int64_t a_rows, int64_t K, int64_t N, int64_t E, int64_t numel);
+int launch_mxfp4_rs(const void* A, int64_t a_rows, int64_t K, const uint8_t* w, const uint8_t* ws,
+                    int64_t E, int64_t N, int64_t numel, int64_t a_row_div,
+                    const int32_t* sorted_ids, const int32_t* offsets, const int32_t* topk_ids,
+                    const int32_t* emap, int num_global, float* planes, hipStream_t stream);
+bool int4_rs_self_route_ok(int64_t numel);
+int launch_mxfp4_swiglu(const float* planes, int S, int64_t numel, int64_t ispp, const uint16_t* b13,
+                        const int32_t* topk_ids, const int32_t* emap, int num_global, int num_local,
+                        float limit, uint16_t* act, hipStream_t stream);
 
 namespace {
 
@@ -309,11 +320,42 @@ int xk_moe_topk_softmax(const void* gating_output, int32_t dtype, int64_t M, int
                              topk_ids, stream);
 }
 
+}  // extern "C"
+
+namespace {
+
+// The MXFP4 pipeline: both projections through the stream kernel (bf16
+// activations, shapes within its limits), else the per-stage kernels.
+// Workspace after the align scratch: act [numel, ispp] bf16, then the down
+// projection's rows [S1, numel, hidden] fp32, then (stream path) the gate/up
+// planes [S0, numel, 2 ispp] fp32.
+struct Mxfp4Plan {
+  bool stream;
+  int s0, s1;
+  int64_t act, down, gu, total;
+  Mxfp4Plan(int64_t M, int64_t top_k, int64_t E, int64_t hidden, int64_t ispp, int a_dtype) {
+    const int64_t numel = M * top_k;
+    AlignScratch al(numel, int(E), mxfp4_block_size());
+    stream = a_dtype == XK_DT_BF16 && numel > 0 && mxfp4_rs_ok(M, hidden, 2 * ispp, E, numel) &&
+             mxfp4_rs_ok(numel, ispp, hidden, E, numel);
+    s0 = stream ? mxfp4_rs_slices(hidden, 2 * ispp, numel, E) : 0;
+    s1 = stream ? mxfp4_rs_slices(ispp, hidden, numel, E) : 1;
+    act = al.total;
+    down = act + round_up(numel * ispp * 2);
+    gu = down + round_up(s1 * numel * hidden * 4);
+    total = gu + round_up(s0 * numel * 2 * ispp * 4);
+  }
+};
+
+}  // namespace
+
+extern "C" {
+
 int64_t xk_moe_mxfp4_workspace_bytes(int64_t M, int64_t top_k, int64_t E, int64_t hidden,
                                      int64_t ispp) {
-  const int64_t numel = M * top_k;
-  AlignScratch al(numel, int(E), mxfp4_block_size());
-  return al.total + round_up(numel * ispp * 2) + round_up(numel * hidden * 4);
+  // the larger of the two plans (the activation dtype is not an argument)
+  return std::max(Mxfp4Plan(M, top_k, E, hidden, ispp, XK_DT_BF16).total,
+                  Mxfp4Plan(M, top_k, E, hidden, ispp, XK_DT_FP32).total);
 }
 
 int xk_moe_mxfp4(const void* A, int32_t a_dtype, int64_t M, int64_t hidden, const uint8_t* w13,
@@ -340,15 +382,38 @@ int xk_moe_mxfp4(const void* A, int32_t a_dtype, int64_t M, int64_t hidden, cons
                      (long long)workspace_bytes, (long long)need);
   const int64_t numel = M * top_k;
   AlignScratch al(numel, int(E), mxfp4_block_size());
-  uint16_t* act = at<uint16_t>(workspace, al.total);
-  float* slot_out = at<float>(workspace, al.total + round_up(numel * ispp * 2));
+  const Mxfp4Plan plan(M, top_k, E, hidden, ispp, a_dtype);
+  uint16_t* act = at<uint16_t>(workspace, plan.act);
+  float* slot_out = at<float>(workspace, plan.down);
   int32_t* sorted = at<int32_t>(workspace, al.sorted);
   int32_t* offsets = at<int32_t>(workspace, al.offsets);
-  int rc = launch_align(topk_ids, numel, int(E), mxfp4_block_size(), expert_map,
-                        num_global_experts, sorted, at<int32_t>(workspace, al.expert_ids),
-                        at<int32_t>(workspace, al.num_post), offsets,
-                        at<char>(workspace, al.inner), al.total - al.inner, stream);
-  if (rc) return rc;
+  // the stream kernels route small batches themselves (no align kernel)
+  const bool self_route = plan.stream && int4_rs_self_route_ok(numel);
+  int rc = XK_OK;
+  if (!self_route) {
+    rc = launch_align(topk_ids, numel, int(E), mxfp4_block_size(), expert_map, num_global_experts,
+                      sorted, at<int32_t>(workspace, al.expert_ids),
+                      at<int32_t>(workspace, al.num_post), offsets, at<char>(workspace, al.inner),
+                      al.total - al.inner, stream);
+    if (rc) return rc;
+  }
+  if (plan.stream) {
+    const int32_t* rs_sorted = self_route ? nullptr : sorted;
+    const int32_t* rs_offsets = self_route ? nullptr : offsets;
+    float* gu = at<float>(workspace, plan.gu);
+    rc = launch_mxfp4_rs(A, M, hidden, w13, w13_scale, E, 2 * ispp, numel, top_k, rs_sorted,
+                         rs_offsets, topk_ids, expert_map, num_global_experts, gu, stream);
+    if (rc) return rc;
+    rc = launch_mxfp4_swiglu(gu, plan.s0, numel, ispp, b13, topk_ids, expert_map,
+                             num_global_experts, int(E), swiglu_limit, act, stream);
+    if (rc) return rc;
+    rc = launch_mxfp4_rs(act, numel, ispp, w2, w2_scale, E, hidden, numel, 1, rs_sorted, rs_offsets,
+                         topk_ids, expert_map, num_global_experts, slot_out, stream);
+    if (rc) return rc;
+    return launch_topk_combine(slot_out, M, top_k, hidden, topk_w, mul_routed_weight, topk_ids,
+                               int(E), expert_map, num_global_experts, out, a_dtype, plan.s1, stream,
+                               b2, 1);
+  }
   rc = launch_mxfp4_stage(0, A, a_dtype, w13, w13_scale, b13, E, hidden, 2 * ispp, ispp, sorted,
                           offsets, numel, top_k, swiglu_limit, act, nullptr, stream);
   if (rc) return rc;

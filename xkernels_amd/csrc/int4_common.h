@@ -167,4 +167,27 @@ __device__ __forceinline__ int count_active_experts(const int32_t* offsets, int 
   return n;
 }
 
+// e8m0 byte -> the scale operand of v_cvt_scalef32_pk_bf16_fp4, which applies
+// only the exponent field of its f32 operand: the byte placed there gives
+// 2^(b-127), byte 0 included (2^-127, as in the reference). Byte 0xFF (the
+// reserved NaN code, which the reference reads as 0) is handled by zeroing the
+// weight word instead (and the scale operand then must not be the inf/nan
+// exponent, which would turn 0 * scale into nan).
+__device__ __forceinline__ float e8m0_scale(uint32_t b) {
+  return __uint_as_float((b == 0xFFu ? 127u : b) << 23);
+}
+
+// 8 e2m1 nibbles of `w` (low nibble = lower k) times `s` -> 8 bf16.
+__device__ __forceinline__ bf16x8 fp4x8_to_bf16(uint32_t w, float s) {
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  const bf16x2 p0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, s, 0);
+  const bf16x2 p1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, s, 1);
+  const bf16x2 p2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, s, 2);
+  const bf16x2 p3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, s, 3);
+  bf16x8 r;
+  r[0] = p0[0]; r[1] = p0[1]; r[2] = p1[0]; r[3] = p1[1];
+  r[4] = p2[0]; r[5] = p2[1]; r[6] = p3[0]; r[7] = p3[1];
+  return r;
+}
+
 }  // namespace xk

@@ -21,7 +21,8 @@
 //   * the segment's activations (16 rows x K / S bf16, 112 KiB) are loaded
 //     once into LDS by direct-to-LDS loads, already in MFMA operand order (a
 //     1 KiB operand is one ds_read_b128 at lane * 16, conflict-free), in
-//     natural k order, which is the order dequant_rne_nat emits;
+//     natural k order, which is the order dequant_rne_nat emits; rows of pad
+//     slots are not read;
 //   * each wave streams its column pairs with no barrier: a ring of lines
 //     (4 x 16-byte weight loads per 128-byte line of 32 columns) in flight,
 //     one line dequantised and contracted per step;
@@ -89,7 +90,15 @@ constexpr int kRsKeep = XK_RS_KEEP;         // finished column pairs a wave hold
 #define XK_RS_SCLINES 8
 #endif
 constexpr int kRsScLines = XK_RS_SCLINES;   // lines per block of group scales (4 or 8)
-constexpr int kRsScLoads = kRsScLines / 4;  // 16-byte scale loads per lane and column tile
+// Weight formats of the stream: the INT4 W4A16 layout (uint4 nibbles, bf16
+// group scales, zero point 8) and MXFP4 (e2m1 nibbles, e8m0 group scales).
+// Both pack 32 elements of a group into 16 bytes, low nibble first.
+constexpr int kFmtInt4 = 0, kFmtFp4 = 1;
+template <int FMT> struct RsFmt {
+  static constexpr int kScaleBytes = FMT == kFmtInt4 ? 2 : 1;  // per group
+  static constexpr int kLinesPerLoad = 16 / (8 * kScaleBytes);  // lines per 16-byte scale load
+  static constexpr int kScLoads = kRsScLines / (4 * kLinesPerLoad);  // per lane and column tile
+};
 constexpr int kRsRing = XK_RS_RING;         // ring slots: lines k+1 .. k+R-1 in flight while line k computes
 constexpr int kRsLdsA = 112 * 1024;         // bytes of LDS for one activation slice
 constexpr int kRsMaxE = 256;
@@ -98,7 +107,7 @@ constexpr int kRsMaxSelf = 4096;            // routed slots a workgroup can rout
 struct RsArgs {
   const uint16_t* A;        // [M, K] bf16
   const uint32_t* packed;   // [E, N, K/8]
-  const uint16_t* scale;    // [E, N, K/32] bf16
+  const void* scale;        // [E, N, K/32]: bf16 (INT4) or e8m0 bytes (MXFP4)
   const int32_t* sorted_ids;  // align outputs, or both null: route from topk_ids
   const int32_t* offsets;   // [E+1] padded prefix in slots (multiples of 16)
   const int32_t* topk_ids;  // [numel] (self-routing only)
@@ -106,6 +115,7 @@ struct RsArgs {
   int num_global;
   float* out;               // [S, numel, N] partial planes
   int K, N, E, numel, top_k;
+  int a_row_div;            // A row of slot t: t / a_row_div (top_k: token rows; 1: slot rows)
   int slices;               // S: K slices (16 rows x K / S bf16 fit kRsLdsA)
   uint32_t a_bytes;         // bytes of A (buffer resource range)
 };
@@ -180,9 +190,10 @@ __device__ __forceinline__ f32x4 quad_transpose(f32x4 e) {
   return e;
 }
 
-__global__ void __launch_bounds__(kRsThreads)
-__attribute__((amdgpu_waves_per_eu(kRsWaves / 4, kRsWaves / 4)))
-int4_stream_rne(RsArgs p) {
+template <int FMT>
+__device__ __forceinline__ void stream_body(const RsArgs& p) {
+  using F = RsFmt<FMT>;
+  constexpr int SB = F::kScaleBytes;
   __shared__ __attribute__((aligned(16))) u32x4 a_lds[kRsLdsA / 16];
   __shared__ int pref[kRsMaxE + 1];
   __shared__ int row_slot[16];
@@ -248,7 +259,7 @@ int4_stream_rne(RsArgs p) {
   const int item_end = static_cast<int>(static_cast<int64_t>(total_items) * (grp + 1) / gsz);
 
   const int w_lane = c16 * KW * 4 + q * 16;  // bytes; + 64 h: group 4 h + q of the line
-  const int s_lane = c16 * G * 2;            // bytes: the line's 8 group scales
+  const int s_lane = c16 * G * SB;           // bytes: start of column c16's scale row
   // v_perm_b32 selector: bytes 2q, 2q+1 of a scale word pair -> bits 16-31
   const uint32_t s_sel = ((2u * q + 1) << 24) | ((2u * q) << 16) | 0x0C0Cu;
   const i32x4 ra = make_rsrc(p.A, p.a_bytes);
@@ -287,7 +298,9 @@ int4_stream_rne(RsArgs p) {
       const int t = p.sorted_ids[row0 + c16];
       sid = t < p.numel ? t : -1;
     }
-    const int a_voff = (sid >= 0 ? sid / p.top_k : 0) * K * 2 + q * 64;
+    // rows of pad slots read nothing (an offset past A; their LDS rows only
+    // feed output rows that are never stored)
+    const int a_voff = sid >= 0 ? (sid / p.a_row_div) * K * 2 + q * 64 : (1 << 30);
     for (int blk = wave; blk < nblk; blk += kRsWaves) {
       const int j = blk & 3, h = (blk >> 2) & 1, line = blk >> 3;
       dma_16(ra, &a_lds[blk * 64], a_voff, (s * Ks + line * 256 + 128 * h + 8 * j) * 2);
@@ -333,7 +346,8 @@ int4_stream_rne(RsArgs p) {
     const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint32_t*>(p.packed + static_cast<int64_t>(e) * N * KW), 0, N * KW * 4, 0x00020000);
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint16_t*>(p.scale + static_cast<int64_t>(e) * N * G), 0, N * G * 2, 0x00020000);
+        const_cast<uint8_t*>(static_cast<const uint8_t*>(p.scale) + static_cast<int64_t>(e) * N * G * SB), 0,
+        N * G * SB, 0x00020000);
     // Steps (lines) of the chunk, padded to a multiple of kRsRing with dummy
     // steps that re-load the last line and compute nothing, so that the
     // steady-state loop issues every load unconditionally.
@@ -344,16 +358,17 @@ int4_stream_rne(RsArgs p) {
 
     struct Slot {
       u32x4 w[2][2];  // weights: [column tile][group 4 h + q]
-      u32x4 s[2][kRsScLoads];  // block-start steps: scales of lines + q + 4 i [column tile][i]
+      u32x4 s[2][F::kScLoads];  // block-start steps: scale bytes 16 (q + 4 i) of the block [tile][i]
     };
     Slot rg[kRsRing];
     auto issue = [&](Slot& sl) __attribute__((always_inline)) {
       const int cp = my_lo + pi;
       const int wo = cp * 32 * KW * 4 + s * (Ks >> 1) + pl * 128;
-      const int so = cp * 32 * G * 2 + (s * (Ks >> 5) + pl * 8) * 2;
+      const int so = cp * 32 * G * SB + (s * (Ks >> 5) + pl * 8) * SB;
       // scales: only on the first line of each block, where lane (c16, q)
-      // loads the 16 bytes of lines pl + q + 4 i (16 contiguous bytes per
-      // column and line of the block)
+      // loads bytes 16 (q + 4 i) .. + 15 of the block's scales (lines pl +
+      // (q + 4 i) L .. + L - 1, L = 16-byte loads per line; contiguous bytes
+      // per column)
       const bool blk = (pl & (kRsScLines - 1)) == 0 && pst < steps;
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
@@ -363,10 +378,10 @@ int4_stream_rne(RsArgs p) {
                                                              XK_RS_LOAD_POLICY);
         if (blk) {  // lanes past the slice's last line read nothing (offset past the buffer)
 #pragma unroll
-          for (int i = 0; i < kRsScLoads; ++i)
+          for (int i = 0; i < F::kScLoads; ++i)
             sl.s[c][i] = __builtin_amdgcn_raw_buffer_load_b128(
-                rs, pl + q + 4 * i < nl ? s_lane + 16 * (q + 4 * i) : (1 << 30), so + c * 16 * G * 2,
-                XK_RS_LOAD_POLICY);
+                rs, pl + (q + 4 * i) * F::kLinesPerLoad < nl ? s_lane + 16 * (q + 4 * i) : (1 << 30),
+                so + c * 16 * G * SB, XK_RS_LOAD_POLICY);
         }
       }
       // advance (value selects keep the cursor in scalar registers)
@@ -383,23 +398,40 @@ int4_stream_rne(RsArgs p) {
 
     auto compute = [&](const Slot& sl) __attribute__((always_inline)) {
       const int lbase = cl * (8 * 64) + lane;
-      // block start: the loaded scales go to this wave's LDS area (line L of
-      // the block at 16 L + c16), then every step reads its own line there
-      u32x4 sv[2];
-      if ((cl & (kRsScLines - 1)) == 0) {
+      // block start: the loaded scales go to this wave's LDS area (16-byte
+      // piece i of the block at 16 i + c16), then every step reads its own
+      // line there
+      const int lb = cl & (kRsScLines - 1);
+      if (lb == 0) {
 #pragma unroll
         for (int c = 0; c < 2; ++c)
 #pragma unroll
-          for (int i = 0; i < kRsScLoads; ++i) sc_lds[wave][c][i * 64 + lane] = sl.s[c][i];
+          for (int i = 0; i < F::kScLoads; ++i) sc_lds[wave][c][i * 64 + lane] = sl.s[c][i];
       }
+      u32x4 sv[2];     // INT4: the line's 8 bf16 scales
+      uint2 sb[2];     // MXFP4: the line's 8 e8m0 bytes
 #pragma unroll
-      for (int c = 0; c < 2; ++c) sv[c] = sc_lds[wave][c][(cl & (kRsScLines - 1)) * 16 + c16];
+      for (int c = 0; c < 2; ++c) {
+        if constexpr (FMT == kFmtInt4)
+          sv[c] = sc_lds[wave][c][lb * 16 + c16];
+        else
+          sb[c] = reinterpret_cast<const uint2*>(&sc_lds[wave][c][0])[((lb >> 1) * 16 + c16) * 2 + (lb & 1)];
+      }
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         RneScale ks[2];
+        float fs[2];
+        bool fnan[2];
 #pragma unroll
-        for (int c = 0; c < 2; ++c)  // bf16 scale of group 4 h + q -> fp32 (one v_perm_b32)
-          ks[c] = rne_scale(__uint_as_float(__builtin_amdgcn_perm(sv[c][2 * h + 1], sv[c][2 * h], s_sel)));
+        for (int c = 0; c < 2; ++c) {
+          if constexpr (FMT == kFmtInt4) {  // bf16 scale of group 4 h + q -> fp32 (one v_perm_b32)
+            ks[c] = rne_scale(__uint_as_float(__builtin_amdgcn_perm(sv[c][2 * h + 1], sv[c][2 * h], s_sel)));
+          } else {  // e8m0 byte of group 4 h + q: byte q of word h
+            const uint32_t b = ((h ? sb[c].y : sb[c].x) >> (8 * q)) & 0xFFu;
+            fs[c] = e8m0_scale(b);
+            fnan[c] = b == 0xFFu;
+          }
+        }
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           bf16x8 bfrag[2];
@@ -408,7 +440,10 @@ int4_stream_rne(RsArgs p) {
 #if XK_RS_VARIANT == 3
             bfrag[c] = __builtin_bit_cast(bf16x8, sl.w[c][h]);
 #else
-            bfrag[c] = dequant_rne_nat(sl.w[c][h][j], ks[c], kNibMask, kNibMaskHi);
+            if constexpr (FMT == kFmtInt4)
+              bfrag[c] = dequant_rne_nat(sl.w[c][h][j], ks[c], kNibMask, kNibMaskHi);
+            else
+              bfrag[c] = fp4x8_to_bf16(fnan[c] ? 0u : sl.w[c][h][j], fs[c]);
 #endif
           }
 #if XK_RS_VARIANT == 2 || XK_RS_VARIANT == 3
@@ -518,6 +553,23 @@ int4_stream_rne(RsArgs p) {
   write_kept();
 }
 
+__global__ void __launch_bounds__(kRsThreads)
+__attribute__((amdgpu_waves_per_eu(kRsWaves / 4, kRsWaves / 4)))
+int4_stream_rne(RsArgs p) {
+  stream_body<kFmtInt4>(p);
+}
+
+// The same stream over MXFP4 weights (e2m1 nibbles, one e8m0 scale byte per
+// 32-element group: 2^(b - 127), byte 0xFF read as 0): each 8-nibble word
+// becomes 8 bf16 with four v_cvt_scalef32_pk_bf16_fp4 (exact: an e2m1 value
+// times a power of two). Used for both MXFP4 MoE projections, whose fp32
+// partial planes are finished by the activation and combine kernels.
+__global__ void __launch_bounds__(kRsThreads)
+__attribute__((amdgpu_waves_per_eu(kRsWaves / 4, kRsWaves / 4)))
+mxfp4_stream_rs(RsArgs p) {
+  stream_body<kFmtFp4>(p);
+}
+
 }  // namespace
 
 // K slices for one 16-row pass: the fewest (K / 256 split evenly) whose
@@ -545,10 +597,47 @@ int launch_int4_rs(const void* A, int64_t M, int64_t K, const int32_t* packed,
                    const int32_t* emap, int num_global, float* slot_out, hipStream_t stream) {
   RsArgs a{static_cast<const uint16_t*>(A), reinterpret_cast<const uint32_t*>(packed), scale,
            sorted_ids, offsets, topk_ids, emap, num_global, slot_out, int(K), int(N), int(E),
-           int(numel), int(top_k), rs_slices(K), static_cast<uint32_t>(M * K * 2)};
+           int(numel), int(top_k), int(top_k), rs_slices(K), static_cast<uint32_t>(M * K * 2)};
   hipLaunchKernelGGL(int4_stream_rne, dim3(static_cast<unsigned>(device_cu_count())),
                      dim3(kRsThreads), 0, stream, a);
   XK_CHECK_LAUNCH("int4_stream_rne");
+  return XK_OK;
+}
+
+#ifndef XK_MX_ITEMS_PER_WAVE
+#define XK_MX_ITEMS_PER_WAVE 8
+#endif
+
+// K slices of an MXFP4 projection: as many as the LDS needs, and more (up to
+// the slice count that still divides the lines) while the work items would
+// give a wave of the grid fewer than XK_MX_ITEMS_PER_WAVE column pairs, since
+// a workgroup's waves finish together only if each holds several items. The
+// estimate takes every routed slot on its own expert (at most E).
+int mxfp4_rs_slices(int64_t K, int64_t N, int64_t numel, int64_t E) {
+  int s = rs_slices(K);
+  if (s == 0) return 0;
+  const int64_t lines = K / 256, waves = int64_t(device_cu_count()) * kRsWaves;
+  const int64_t pairs = std::min(E, numel) * (N / 32);
+  while (pairs * s < XK_MX_ITEMS_PER_WAVE * waves && lines % (2 * s) == 0) s *= 2;
+  return s;
+}
+
+bool mxfp4_rs_ok(int64_t a_rows, int64_t K, int64_t N, int64_t E, int64_t numel) {
+  const int s = K % 256 == 0 ? mxfp4_rs_slices(K, N, numel, E) : 0;
+  return s > 0 && N % 32 == 0 && E <= kRsMaxE && N * (K / 2) < (int64_t(1) << 31) &&
+         a_rows * K * 2 < (int64_t(1) << 31) && numel * N * 4 * s < (int64_t(1) << 31);
+}
+
+int launch_mxfp4_rs(const void* A, int64_t a_rows, int64_t K, const uint8_t* w, const uint8_t* ws,
+                    int64_t E, int64_t N, int64_t numel, int64_t a_row_div,
+                    const int32_t* sorted_ids, const int32_t* offsets, const int32_t* topk_ids,
+                    const int32_t* emap, int num_global, float* planes, hipStream_t stream) {
+  RsArgs a{static_cast<const uint16_t*>(A), reinterpret_cast<const uint32_t*>(w), ws, sorted_ids,
+           offsets, topk_ids, emap, num_global, planes, int(K), int(N), int(E), int(numel), 1,
+           int(a_row_div), mxfp4_rs_slices(K, N, numel, E), static_cast<uint32_t>(a_rows * K * 2)};
+  hipLaunchKernelGGL(mxfp4_stream_rs, dim3(static_cast<unsigned>(device_cu_count())),
+                     dim3(kRsThreads), 0, stream, a);
+  XK_CHECK_LAUNCH("mxfp4_stream_rs");
   return XK_OK;
 }
 

@@ -28,29 +28,6 @@ constexpr int kChunkK = kChunkGroups * 32;
 constexpr int kRows = 32;                 // slots per pass (two MFMA row tiles)
 constexpr int kStride = kChunkK + 8;      // bf16 elements per LDS row
 
-// e8m0 byte -> the scale operand of v_cvt_scalef32_pk_bf16_fp4, which applies
-// only the exponent field of its f32 operand: the byte placed there gives
-// 2^(b-127), byte 0 included (2^-127, as in the reference). Byte 0xFF (the
-// reserved NaN code, which the reference reads as 0) is handled by zeroing the
-// weight word instead (and the scale operand then must not be the inf/nan
-// exponent, which would turn 0 * scale into nan).
-__device__ __forceinline__ float e8m0_scale(uint32_t b) {
-  return __uint_as_float((b == 0xFFu ? 127u : b) << 23);
-}
-
-// 8 e2m1 nibbles of `w` (low nibble = lower k) times `s` -> 8 bf16.
-__device__ __forceinline__ bf16x8 fp4x8_to_bf16(uint32_t w, float s) {
-  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-  const bf16x2 p0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, s, 0);
-  const bf16x2 p1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, s, 1);
-  const bf16x2 p2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, s, 2);
-  const bf16x2 p3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, s, 3);
-  bf16x8 r;
-  r[0] = p0[0]; r[1] = p0[1]; r[2] = p1[0]; r[3] = p1[1];
-  r[4] = p2[0]; r[5] = p2[1]; r[6] = p3[0]; r[7] = p3[1];
-  return r;
-}
-
 // Stages one 32 x 256 activation chunk into LDS (bf16). Row r of the pass reads
 // source row src_row[r] (< 0: zero row); TA is the activation storage type.
 template <typename TA>
@@ -668,6 +645,52 @@ mxfp4_down_smallk(Mxfp4V2Args args) {
   }
 }
 
+// Gate/up epilogue for the stream path: the projection's S fp32 partial planes
+// [S, numel, 2 ispp] are summed and finished exactly like the per-workgroup
+// epilogue above: gu = bf16(sum) (+ b13 -> bf16), g clamped from above, u on
+// both sides, act = bf16(silu(g) * u). Four columns per thread; slots whose
+// expert is not local (never computed) are skipped.
+__global__ void __launch_bounds__(256)
+mxfp4_swiglu_planes(const float* __restrict__ planes, int S, int64_t numel, int ispp,
+                    const uint16_t* __restrict__ b13, const int32_t* __restrict__ topk_ids,
+                    const int32_t* __restrict__ emap, int num_global, int num_local, float limit,
+                    uint16_t* __restrict__ act) {
+  const int64_t per_row = ispp / 4;
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (idx >= numel * per_row) return;
+  const int64_t t = idx / per_row;
+  const int j0 = static_cast<int>(idx - t * per_row) * 4;
+  const int e = map_expert(topk_ids[t], emap, num_global, num_local);
+  if (e < 0) return;
+  const int64_t pstride = numel * 2 * ispp;
+  const float* row = planes + t * 2 * ispp;
+  f32x4 g = *reinterpret_cast<const f32x4*>(row + j0);
+  f32x4 u = *reinterpret_cast<const f32x4*>(row + ispp + j0);
+  for (int sl = 1; sl < S; ++sl) {
+    g += *reinterpret_cast<const f32x4*>(row + sl * pstride + j0);
+    u += *reinterpret_cast<const f32x4*>(row + sl * pstride + ispp + j0);
+  }
+  uint16_t r[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    float gv = round_bf16(g[i]), uv = round_bf16(u[i]);
+    if (b13 != nullptr) {
+      const uint16_t* b = b13 + static_cast<int64_t>(e) * 2 * ispp;
+      gv = round_bf16(gv + bf16_to_f32(b[j0 + i]));
+      uv = round_bf16(uv + bf16_to_f32(b[ispp + j0 + i]));
+    }
+    if (limit > 0.f) {
+      gv = fminf(gv, limit);
+      uv = fminf(fmaxf(uv, -limit), limit);
+    }
+    r[i] = f32_to_bf16((gv / (1.0f + __expf(-gv))) * uv);
+  }
+  uint2 o;
+  o.x = r[0] | (static_cast<uint32_t>(r[1]) << 16);
+  o.y = r[2] | (static_cast<uint32_t>(r[3]) << 16);
+  *reinterpret_cast<uint2*>(act + t * ispp + j0) = o;
+}
+
 }  // namespace
 
 int device_cu_count();
@@ -721,6 +744,23 @@ int launch_mxfp4_stage(int stage, const void* A, int a_dtype, const uint8_t* w,
     hipLaunchKernelGGL((mxfp4_stream_gemm<1, uint16_t>), grid, dim3(256), 0, stream, a);
     XK_CHECK_LAUNCH("mxfp4_stream_gemm<1>");
   }
+  return XK_OK;
+}
+
+}  // namespace xk
+
+namespace xk {
+
+int launch_mxfp4_swiglu(const float* planes, int S, int64_t numel, int64_t ispp, const uint16_t* b13,
+                        const int32_t* topk_ids, const int32_t* emap, int num_global, int num_local,
+                        float limit, uint16_t* act, hipStream_t stream) {
+  XK_REQUIRE(ispp % 4 == 0, "mxfp4 swiglu: ispp %lld not a multiple of 4", (long long)ispp);
+  const int64_t n = numel * (ispp / 4);
+  if (n == 0) return XK_OK;
+  hipLaunchKernelGGL(mxfp4_swiglu_planes, dim3(static_cast<unsigned>(cdiv(n, 256))), dim3(256), 0,
+                     stream, planes, S, numel, int(ispp), b13, topk_ids, emap, num_global, num_local,
+                     limit, act);
+  XK_CHECK_LAUNCH("mxfp4_swiglu_planes");
   return XK_OK;
 }
 

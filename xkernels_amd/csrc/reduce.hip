@@ -85,6 +85,11 @@ struct RowWeights {
   const int32_t* ids;   // [M, top_k] or null (no mask)
   const int32_t* emap;  // nullable
   int num_global, num_local;
+  // MXFP4 down projection finished here: a slot's summed row is rounded to
+  // bf16, then bias[expert] is added and the sum rounded to bf16 again
+  // (the reference's bf16 matmul output and bias add)
+  const uint16_t* post_bias = nullptr;  // [num_local, H] bf16 or null
+  int post_round = 0;
 
   __device__ __forceinline__ float get(int64_t idx) const {
     if (w == nullptr) return 1.0f;
@@ -95,6 +100,17 @@ struct RowWeights {
   // selected away rather than multiplied by zero).
   __device__ __forceinline__ bool valid(int64_t idx) const {
     return ids == nullptr || map_expert(ids[idx], emap, num_global, num_local) >= 0;
+  }
+  template <int VEC>
+  __device__ __forceinline__ void post(int64_t idx, int64_t H, int64_t h, float* v) const {
+    if (!post_round) return;
+    const int e = ids == nullptr ? -1 : map_expert(ids[idx], emap, num_global, num_local);
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) {
+      v[i] = round_bf16(v[i]);
+      if (post_bias != nullptr && e >= 0)
+        v[i] = round_bf16(v[i] + bf16_to_f32(post_bias[static_cast<int64_t>(e) * H + h + i]));
+    }
   }
 };
 
@@ -134,9 +150,11 @@ topk_reduce(const Tin* __restrict__ y, int64_t M, int top_k_rt, int64_t H, RowWe
       }
     }
 #pragma unroll
-    for (int k = 0; k < KFIX; ++k)
+    for (int k = 0; k < KFIX; ++k) {
+      rw.template post<VEC>(m * top_k + k, H, h, v[k]);
 #pragma unroll
       for (int i = 0; i < VEC; ++i) acc[i] += ok[k] ? v[k][i] * wk[k] : 0.0f;
+    }
   } else {
     for (int k = 0; k < top_k; ++k) {
       if (!rw.valid(m * top_k + k)) continue;
@@ -149,6 +167,7 @@ topk_reduce(const Tin* __restrict__ y, int64_t M, int top_k_rt, int64_t H, RowWe
 #pragma unroll
         for (int i = 0; i < VEC; ++i) v[i] += t[i];
       }
+      rw.template post<VEC>(m * top_k + k, H, h, v);
 #pragma unroll
       for (int i = 0; i < VEC; ++i) acc[i] += v[i] * wk;
     }
@@ -220,7 +239,8 @@ int launch_sum_reduce(const void* y, int y_dtype, int64_t M, int64_t top_k, int6
 int launch_topk_combine(const float* slot_out, int64_t M, int64_t top_k, int64_t N,
                         const float* topk_w, int mul_routed_weight, const int32_t* topk_ids,
                         int num_local, const int32_t* emap, int num_global, void* out,
-                        int out_dtype, int nparts, hipStream_t stream) {
+                        int out_dtype, int nparts, hipStream_t stream, const uint16_t* post_bias,
+                        int post_round) {
   XK_REQUIRE(nparts >= 1 && nparts <= 64, "combine: nparts=%d outside [1, 64]", nparts);
   XK_REQUIRE(out_dtype == XK_DT_BF16 || out_dtype == XK_DT_FP32, "combine: bad out dtype %d",
              out_dtype);
@@ -228,7 +248,7 @@ int launch_topk_combine(const float* slot_out, int64_t M, int64_t top_k, int64_t
   XK_REQUIRE(top_k >= 1 && top_k <= 1024, "combine: top_k=%lld outside [1, 1024]",
              (long long)top_k);
   const RowWeights rw{mul_routed_weight ? topk_w : nullptr, XK_DT_FP32, topk_ids, emap,
-                      num_global, num_local};
+                      num_global, num_local, post_bias, post_round};
   const int64_t pstride = M * top_k * N;
   if (out_dtype == XK_DT_BF16)
     return launch_reduce(slot_out, M, int(top_k), N, rw, 1.0f, static_cast<uint16_t*>(out),
