@@ -69,6 +69,18 @@ def test_size_queries():
     assert wm >= 288 * 512 * 2 + 288 * 4096 * 4
 
 
+@pytest.mark.parametrize("E,hidden,ispp,top_k", [(256, 4096, 512, 6), (8, 256, 256, 2), (32, 512, 512, 4)])
+def test_mxfp4_workspace_never_shrinks_with_batch(E, hidden, ispp, top_k):
+    """A workspace sized for a batch must serve every smaller batch: the stream
+    path cuts K into more slices for small batches, so its partial planes are
+    sized for the largest slices x slots over the smaller sizes."""
+    prev = 0
+    for M in range(1, 70):
+        b = _lib.query("xk_moe_mxfp4_workspace_bytes", M, top_k, E, hidden, ispp)
+        assert b >= prev, (M, b, prev)
+        prev = b
+
+
 def _rc(name, *args):
     return getattr(_lib.load(), name)(*args)
 

@@ -38,9 +38,16 @@ def _ref(A, wts, ids, w, **kw):
     return moe_mxfp4_ref(A, *(wts[k] for k in KEYS), ids, w, b13=wts["b13"], b2=wts["b2"], **kw)
 
 
+# hidden and ispp multiples of 256 (bf16 A): both projections run the stream
+# kernel (fp32 partial planes, SwiGLU and combine kernels); other shapes the
+# per-stage kernels
+STREAM_SHAPES = [(4, 8, 256, 256, 2), (1, 16, 512, 256, 6), (48, 32, 512, 512, 6),
+                 (33, 4, 256, 512, 2), (200, 64, 256, 256, 8)]
+
+
 @pytest.mark.parametrize("M,E,hidden,ispp,top_k", [(4, 8, 256, 64, 2), (1, 16, 512, 128, 6),
                                                    (7, 8, 256, 96, 3), (48, 32, 512, 64, 6),
-                                                   (40, 4, 128, 32, 2)])
+                                                   (40, 4, 128, 32, 2)] + STREAM_SHAPES)
 @pytest.mark.parametrize("bias", [False, True])
 @pytest.mark.parametrize("mul_routed", [True, False])
 def test_matches_oracle(M, E, hidden, ispp, top_k, bias, mul_routed, dev):
@@ -50,9 +57,10 @@ def test_matches_oracle(M, E, hidden, ispp, top_k, bias, mul_routed, dev):
     assert_close(got, _ref(A, wts, ids, w, mul_routed_weight=mul_routed), 2e-2, 2e-2, "mxfp4")
 
 
+@pytest.mark.parametrize("ispp", [64, 256])
 @pytest.mark.parametrize("limit", [None, 0.0, 1.5])
-def test_swiglu_limit(limit, dev):
-    A, wts, ids, w = _case(6, 8, 256, 64, 2, seed=4)
+def test_swiglu_limit(limit, ispp, dev):
+    A, wts, ids, w = _case(6, 8, 256, ispp, 2, seed=4)
     got = _run(A, wts, ids, w, dev, swiglu_limit=limit)
     assert_close(got, _ref(A, wts, ids, w, swiglu_limit=limit), 2e-2, 2e-2, f"limit={limit}")
 
@@ -87,10 +95,11 @@ def test_decode_is_exact_single_slot(dev):
     assert_close(got, want, 1e-2, 1e-2, "single slot")
 
 
+@pytest.mark.parametrize("ispp", [64, 256])
 @pytest.mark.parametrize("ep_size", [2, 4])
-def test_expert_parallel_partials(ep_size, dev):
+def test_expert_parallel_partials(ep_size, ispp, dev):
     E, M = 16, 10
-    A, wts, ids, w = _case(M, E, 256, 64, 4, seed=9)
+    A, wts, ids, w = _case(M, E, 256, ispp, 4, seed=9)
     dense = _run(A, wts, ids, w, dev).float()
     per = E // ep_size
     total = torch.zeros_like(dense)
@@ -104,10 +113,13 @@ def test_expert_parallel_partials(ep_size, dev):
     assert_close(total, dense, 3e-2, 3e-2, "EP sum")
 
 
-def test_workspace(dev):
-    ws = MoeMxfp4Workspace.allocate(16, 2, 8, 16, 64, 256, dtype=torch.bfloat16, device=dev)
+@pytest.mark.parametrize("ispp", [64, 256])
+def test_workspace(ispp, dev):
+    """One workspace, sized for M=16, serves M=16 and then M=3 (the stream path
+    uses more K slices at M=3)."""
+    ws = MoeMxfp4Workspace.allocate(16, 2, 8, 16, ispp, 256, dtype=torch.bfloat16, device=dev)
     for M in (16, 3):
-        A, wts, ids, w = _case(M, 8, 256, 64, 2, seed=M)
+        A, wts, ids, w = _case(M, 8, 256, ispp, 2, seed=M)
         got = _run(A, wts, ids, w, dev, workspace=ws)
         assert_close(got, _ref(A, wts, ids, w), 2e-2, 2e-2, f"ws M={M}")
 

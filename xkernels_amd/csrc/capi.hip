@@ -328,7 +328,17 @@ namespace {
 // activations, shapes within its limits), else the per-stage kernels.
 // Workspace after the align scratch: act [numel, ispp] bf16, then the down
 // projection's rows [S1, numel, hidden] fp32, then (stream path) the gate/up
-// planes [S0, numel, 2 ispp] fp32.
+// planes [S0, numel, 2 ispp] fp32. The slice counts grow as batches shrink,
+// so each plane region is sized for the largest S(n) n over n <= numel: the
+// workspace bytes never decrease with M, and a workspace sized for a batch
+// serves every smaller one.
+int64_t max_plane_rows(int64_t K, int64_t N, int64_t numel, int64_t E) {
+  int64_t best = mxfp4_rs_slices(K, N, numel, E) * numel;
+  for (int64_t n = 1; n < std::min(numel, E); ++n)  // S(n) is constant from n = E on
+    best = std::max<int64_t>(best, mxfp4_rs_slices(K, N, n, E) * n);
+  return best;
+}
+
 struct Mxfp4Plan {
   bool stream;
   int s0, s1;
@@ -342,8 +352,8 @@ struct Mxfp4Plan {
     s1 = stream ? mxfp4_rs_slices(ispp, hidden, numel, E) : 1;
     act = al.total;
     down = act + round_up(numel * ispp * 2);
-    gu = down + round_up(s1 * numel * hidden * 4);
-    total = gu + round_up(s0 * numel * 2 * ispp * 4);
+    gu = down + round_up((stream ? max_plane_rows(ispp, hidden, numel, E) : numel) * hidden * 4);
+    total = gu + round_up(stream ? max_plane_rows(hidden, 2 * ispp, numel, E) * 2 * ispp * 4 : 0);
   }
 };
 

@@ -1,4 +1,4 @@
-// Grouped MXFP4 MoE GEMMs for gfx950 (the reference's _mxfp4_moe_gemm_kernel,
+// MXFP4 MoE kernels for gfx950 (the reference's _mxfp4_moe_gemm_kernel,
 // src/xkernels/ops/moe/triton/moe_mxfp4_kernel.py:87-352; math of the oracle
 // mxfp4_reference.py:28-112 with the dequant of ops/gather/mxfp4.py:39-68).
 //
@@ -8,13 +8,15 @@
 // followed by the weighted top-k combine (reduce.hip). The bf16 roundings sit
 // where the reference's bf16 torch ops round (matmul output, bias add, act).
 //
-// Both stages stream each active expert's packed weights once (decode regime):
-// a workgroup owns (expert e, a column block) and all of e's routed slots,
-// 32 at a time. Lane (c, q) of a wave reads 16 bytes = one 32-element e8m0
-// group of its weight row and dequantises it with four
-// v_cvt_scalef32_pk_bf16_fp4 (two e2m1 -> two bf16, times 2^(e-127), exact), so
-// the bf16 operands feed v_mfma_f32_16x16x32_bf16 directly; each 16-byte load
-// yields four MFMAs. A 32-row x 256-k activation chunk is staged in LDS.
+// Main path (bf16 activations, hidden and ispp multiples of 256, E <= 256):
+// both projections run mxfp4_stream_rs (int4_stream.hip) into fp32 partial
+// planes; mxfp4_swiglu_planes below finishes stage 0 and the combine applies
+// stage 1's roundings and bias. Every other shape runs mxfp4_stream_gemm: a
+// workgroup owns (expert e, a column block) and all of e's routed slots, 32 at
+// a time; lane (c, q) of a wave reads 16 bytes = one 32-element e8m0 group of
+// its weight row and dequantises it with four v_cvt_scalef32_pk_bf16_fp4 (two
+// e2m1 -> two bf16, times 2^(e-127), exact); a 32-row x 256-k activation chunk
+// is staged in LDS.
 #include <algorithm>
 #include <type_traits>
 
@@ -236,415 +238,6 @@ mxfp4_stream_gemm(Mxfp4Args p) {
   }
 }
 
-// Persistent stream kernel (K a multiple of 256). Same results as
-// mxfp4_stream_gemm; the loop is organised like the INT4 decode stream kernel:
-//   * a grid of 2 x CUs workgroups walks (active expert, column block) items;
-//   * weights of the next three 256-k chunks are in flight in a register ring,
-//     with their 8 e8m0 scale bytes (one 8-byte load per weight row and chunk);
-//     every load is unconditional (clamped) so the compiler never drains the
-//     load counter;
-//   * only the routed rows' activations are staged (the pass body is compiled
-//     for one and for two 16-row tiles), double buffered, one barrier a chunk;
-//   * v_cvt_scalef32_pk_bf16_fp4 applies the scale exponent: the scale operand
-//     is the e8m0 byte placed in an f32 exponent field, so byte 0 is 2^-127 as
-//     in the reference; byte 0xFF (reference: 0) zeroes the weight word.
-struct Mxfp4V2Args {
-  Mxfp4Args p;
-  int num_experts;
-};
-
-template <int STAGE, typename TA>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
-mxfp4_stream_v2(Mxfp4V2Args args) {
-  constexpr int kWaves = 4, kThreads = 256;
-  constexpr int kColsPerWave = STAGE == 0 ? 16 : 32;
-  constexpr int kCols = kWaves * kColsPerWave;
-  constexpr int kAStride = kChunkK + 16;  // bf16 per LDS row (136 dwords)
-  __shared__ __attribute__((aligned(16))) uint16_t a_lds[2][kRows * kAStride];
-  __shared__ int slot_lds[kRows];
-  __shared__ int src_lds[kRows];
-  const Mxfp4Args& p = args.p;
-
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int c16 = lane & 15, q = lane >> 4;
-  const int K = p.K, G = K >> 5, KB = K >> 1;
-  const int nchunks = G / kChunkGroups;
-  const int nb = (p.ncols + kCols - 1) / kCols;
-  const int items = count_active_experts(p.offsets, args.num_experts) * nb;
-
-  for (int item = blockIdx.x; item < items; item += gridDim.x) {
-    const int e = find_active_expert(p.offsets, args.num_experts, item / nb);
-    const int col_base = (item % nb) * kCols + wave * kColsPerWave;
-    const int beg = p.offsets[e], end = p.offsets[e + 1];
-    const uint8_t* wrow[2];
-    const uint8_t* srow[2];
-    int col[2];
-#pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      int row;
-      if (STAGE == 0) {
-        col[c] = col_base + c16;                             // act column j
-        row = min(col[c], p.ncols - 1) + (c ? p.ncols : 0);  // gate row j, up row ispp + j
-      } else {
-        col[c] = col_base + 16 * c + c16;
-        row = min(col[c], p.ncols - 1);
-      }
-      wrow[c] = p.w + (static_cast<int64_t>(e) * p.rows + row) * KB + q * 16;
-      srow[c] = p.ws + (static_cast<int64_t>(e) * p.rows + row) * G;
-    }
-
-    for (int pass = beg; pass < end; pass += kRows) {
-      const int ntiles = min(2, (end - pass) >> 4);
-      __syncthreads();  // previous pass / item done with LDS
-      if (tid < kRows) {
-        int slot = -1, src = -1;
-        if (tid < ntiles * 16) {
-          const int sidx = p.sorted_ids[pass + tid];
-          if (sidx < p.numel) { slot = sidx; src = STAGE == 0 ? sidx / p.top_k : sidx; }
-        }
-        slot_lds[tid] = slot;
-        src_lds[tid] = src;
-      }
-      __syncthreads();
-
-      auto body = [&](auto nt_tag) {
-        constexpr int NT = decltype(nt_tag)::value;
-        // staging: NT*16 rows x 32 vectors of 8 activations per chunk; thread ->
-        // row st_r, vectors v0 .. v0 + kVec - 1 (vector v = 4 g + j)
-        constexpr int kVec = NT * 16 * 32 / kThreads;
-        constexpr int kTPR = 32 / kVec;
-        constexpr int kLoads = kVec * (sizeof(TA) == 4 ? 2 : 1);  // 16-byte loads
-        const int st_r = tid / kTPR, v0 = (tid % kTPR) * kVec;
-        const int my_src = max(src_lds[st_r], 0);  // rows without a slot read row 0
-        const u32x4* a_src = reinterpret_cast<const u32x4*>(static_cast<const TA*>(p.A) +
-                                                            static_cast<int64_t>(my_src) * K) +
-                             v0 * (sizeof(TA) == 4 ? 2 : 1);
-
-        auto load_a = [&](int chunk, u32x4* ar) {
-          chunk = min(chunk, nchunks - 1);
-          constexpr int kPerChunk = kChunkK * sizeof(TA) / 16;
-#pragma unroll
-          for (int i = 0; i < kLoads; ++i) ar[i] = a_src[chunk * kPerChunk + i];
-        };
-        auto store_a = [&](int buf, const u32x4* ar) {
-          // vector (g, j) of a row -> dword (g >> 2) * 64 + j * 16 + (g & 3) * 4:
-          // the 16-byte reads of one MFMA are 4 dwords apart across lane groups
-          // and the 16 rows 136 dwords apart (bank-conflict free)
-          uint32_t* row = reinterpret_cast<uint32_t*>(&a_lds[buf][st_r * kAStride]);
-#pragma unroll
-          for (int i = 0; i < kVec; ++i) {
-            u32x4 v;
-            if constexpr (sizeof(TA) == 4) {
-              const f32x4 x0 = __builtin_bit_cast(f32x4, ar[2 * i]);
-              const f32x4 x1 = __builtin_bit_cast(f32x4, ar[2 * i + 1]);
-              v = u32x4{f32_to_bf16(x0[0]) | (static_cast<uint32_t>(f32_to_bf16(x0[1])) << 16),
-                        f32_to_bf16(x0[2]) | (static_cast<uint32_t>(f32_to_bf16(x0[3])) << 16),
-                        f32_to_bf16(x1[0]) | (static_cast<uint32_t>(f32_to_bf16(x1[1])) << 16),
-                        f32_to_bf16(x1[2]) | (static_cast<uint32_t>(f32_to_bf16(x1[3])) << 16)};
-            } else {
-              v = ar[i];
-            }
-            const int g = (v0 + i) >> 2, j = (v0 + i) & 3;
-            *reinterpret_cast<u32x4*>(row + (g >> 2) * 64 + j * 16 + (g & 3) * 4) = v;
-          }
-        };
-        auto load_w = [&](int chunk, u32x4 (&wr)[2][2], uint2 (&sr)[2]) {
-          chunk = min(chunk, nchunks - 1);
-#pragma unroll
-          for (int c = 0; c < 2; ++c) {
-#pragma unroll
-            for (int h = 0; h < 2; ++h)
-              wr[c][h] = *reinterpret_cast<const u32x4*>(wrow[c] + (chunk * kChunkGroups + 4 * h) * 16);
-            sr[c] = *reinterpret_cast<const uint2*>(srow[c] + chunk * kChunkGroups);
-          }
-        };
-
-        f32x4 acc[2][2];
-#pragma unroll
-        for (int t = 0; t < 2; ++t)
-#pragma unroll
-          for (int c = 0; c < 2; ++c) acc[t][c] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-        auto compute = [&](int buf, const u32x4 (&wr)[2][2], const uint2 (&sr)[2]) {
-#pragma unroll
-          for (int h = 0; h < 2; ++h) {
-            // scale byte of group 4h + q: byte q of word h
-            float sc[2];
-            bool nan[2];
-#pragma unroll
-            for (int c = 0; c < 2; ++c) {
-              const uint32_t b = ((h ? sr[c].y : sr[c].x) >> (8 * q)) & 0xFFu;
-              sc[c] = e8m0_scale(b);
-              nan[c] = b == 0xFFu;
-            }
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-              bf16x8 bfrag[2];
-#pragma unroll
-              for (int c = 0; c < 2; ++c) {
-                typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-                const uint32_t w = nan[c] ? 0u : wr[c][h][j];
-                const bf16x2 p0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc[c], 0);
-                const bf16x2 p1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc[c], 1);
-                const bf16x2 p2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc[c], 2);
-                const bf16x2 p3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc[c], 3);
-                bfrag[c] = bf16x8{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
-              }
-#pragma unroll
-              for (int t = 0; t < NT; ++t) {
-                const bf16x8 afrag = *reinterpret_cast<const bf16x8*>(
-                    &a_lds[buf][(t * 16 + c16) * kAStride + 2 * (h * 64 + j * 16 + q * 4)]);
-#pragma unroll
-                for (int c = 0; c < 2; ++c)
-                  acc[t][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(afrag, bfrag[c], acc[t][c], 0, 0, 0);
-              }
-            }
-          }
-        };
-
-        constexpr int kWRing = 4;
-        u32x4 areg[kLoads];
-        u32x4 w0[2][2], w1[2][2], w2[2][2], w3[2][2];
-        uint2 s0[2], s1[2], s2[2], s3[2];
-        load_a(0, areg);
-        store_a(0, areg);
-        // the rest in the order the loop leaves its loads outstanding at its
-        // head (W(c+1), A(c+1), W(c+2)), so the loop-head wait is not a drain
-        __builtin_amdgcn_sched_barrier(0);
-        load_w(0, w0, s0);
-        __builtin_amdgcn_sched_barrier(0);
-        load_w(1, w1, s1);
-        __builtin_amdgcn_sched_barrier(0);
-        load_a(1, areg);
-        __builtin_amdgcn_sched_barrier(0);
-        load_w(2, w2, s2);
-        __builtin_amdgcn_sched_barrier(0);
-        // step c: A(c+1) -> LDS buffer (c+1)&1 (freed by compute(c-1)); request
-        // A(c+2) and W(c+3); compute chunk c.
-        auto step = [&](int c, const u32x4 (&wc)[2][2], const uint2 (&sc)[2], u32x4 (&wn)[2][2],
-                        uint2 (&sn)[2]) {
-          __syncthreads();
-          store_a((c + 1) & 1, areg);
-          load_a(c + 2, areg);
-          load_w(c + 3, wn, sn);
-          if (c < nchunks) compute(c & 1, wc, sc);
-        };
-        for (int c = 0; c < nchunks; c += kWRing) {
-          step(c, w0, s0, w3, s3);
-          step(c + 1, w1, s1, w0, s0);
-          step(c + 2, w2, s2, w1, s1);
-          step(c + 3, w3, s3, w2, s2);
-        }
-
-#pragma unroll
-        for (int t = 0; t < NT; ++t) {
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int slot = slot_lds[t * 16 + q * 4 + i];
-            if (slot < 0) continue;
-            if (STAGE == 0) {
-              const int j = col[0];
-              if (j >= p.ncols) continue;
-              float g = round_bf16(acc[t][0][i]);
-              float u = round_bf16(acc[t][1][i]);
-              if (p.bias != nullptr) {
-                const uint16_t* b = p.bias + static_cast<int64_t>(e) * 2 * p.ncols;
-                g = round_bf16(g + bf16_to_f32(b[j]));
-                u = round_bf16(u + bf16_to_f32(b[p.ncols + j]));
-              }
-              if (p.limit > 0.f) {
-                g = fminf(g, p.limit);
-                u = fminf(fmaxf(u, -p.limit), p.limit);
-              }
-              const float a = (g / (1.0f + __expf(-g))) * u;
-              p.act[static_cast<int64_t>(slot) * p.ncols + j] = f32_to_bf16(a);
-            } else {
-#pragma unroll
-              for (int c = 0; c < 2; ++c) {
-                const int n = col[c];
-                if (n >= p.ncols) continue;
-                float d = round_bf16(acc[t][c][i]);
-                if (p.bias != nullptr)
-                  d = round_bf16(d + bf16_to_f32(p.bias[static_cast<int64_t>(e) * p.ncols + n]));
-                p.slot_out[static_cast<int64_t>(slot) * p.ncols + n] = d;
-              }
-            }
-          }
-        }
-      };
-      if (ntiles == 2)
-        body(std::integral_constant<int, 2>{});
-      else
-        body(std::integral_constant<int, 1>{});
-    }
-  }
-}
-
-// Down projection with a short contraction (K = ispp <= 512, a multiple of 256):
-// the routed rows' activations for the whole K are staged once per pass (the
-// two LDS chunk buffers hold K = 512), then the workgroup streams the weights of
-// kSpan consecutive 128-column blocks of the expert through the register ring
-// without any further barrier, writing each block's rows as it completes. This
-// keeps the weight stream busy across column blocks, which a per-block prologue
-// (two chunks per block) would not.
-template <int kSpan>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
-mxfp4_down_smallk(Mxfp4V2Args args) {
-  constexpr int kThreads = 256, kCols = 128, kAStride = kChunkK + 16;
-  __shared__ __attribute__((aligned(16))) uint16_t a_lds[2][kRows * kAStride];
-  __shared__ int slot_lds[kRows];
-  __shared__ int src_lds[kRows];
-  const Mxfp4Args& p = args.p;
-
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int c16 = lane & 15, q = lane >> 4;
-  const int K = p.K, G = K >> 5, KB = K >> 1;
-  const int nchunks = G / kChunkGroups;  // 1 or 2
-  const int nspan = (p.ncols + kSpan * kCols - 1) / (kSpan * kCols);
-  const int items = count_active_experts(p.offsets, args.num_experts) * nspan;
-
-  for (int item = blockIdx.x; item < items; item += gridDim.x) {
-    const int e = find_active_expert(p.offsets, args.num_experts, item / nspan);
-    const int span_base = (item % nspan) * kSpan * kCols + wave * 32;
-    const int beg = p.offsets[e], end = p.offsets[e + 1];
-    const int64_t erow = static_cast<int64_t>(e) * p.rows;
-
-    for (int pass = beg; pass < end; pass += kRows) {
-      const int ntiles = min(2, (end - pass) >> 4);
-      __syncthreads();
-      if (tid < kRows) {
-        int slot = -1, src = -1;
-        if (tid < ntiles * 16) {
-          const int sidx = p.sorted_ids[pass + tid];
-          if (sidx < p.numel) { slot = sidx; src = sidx; }
-        }
-        slot_lds[tid] = slot;
-        src_lds[tid] = src;
-      }
-      __syncthreads();
-
-      auto body = [&](auto nt_tag) {
-        constexpr int NT = decltype(nt_tag)::value;
-        constexpr int kVec = NT * 16 * 32 / kThreads;
-        constexpr int kTPR = 32 / kVec;
-        const int st_r = tid / kTPR, v0 = (tid % kTPR) * kVec;
-        const u32x4* a_src = reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(p.A) +
-                                                            static_cast<int64_t>(max(src_lds[st_r], 0)) * K) + v0;
-        // stage every chunk of K once
-        for (int ch = 0; ch < nchunks; ++ch) {
-          uint32_t* row = reinterpret_cast<uint32_t*>(&a_lds[ch][st_r * kAStride]);
-#pragma unroll
-          for (int i = 0; i < kVec; ++i) {
-            const int g = (v0 + i) >> 2, j = (v0 + i) & 3;
-            *reinterpret_cast<u32x4*>(row + (g >> 2) * 64 + j * 16 + (g & 3) * 4) =
-                a_src[ch * (kChunkK / 8) + i];
-          }
-        }
-        __syncthreads();
-
-        // sub-step s = (column block s / nchunks, chunk s % nchunks)
-        const int nsub = kSpan * nchunks;
-        auto load_w = [&](int sub, u32x4 (&wr)[2][2], uint2 (&sr)[2]) {
-          sub = min(sub, nsub - 1);
-          const int cb = sub / nchunks, ch = sub - cb * nchunks;
-#pragma unroll
-          for (int c = 0; c < 2; ++c) {
-            const int row = min(span_base + cb * kCols + 16 * c + c16, p.ncols - 1);
-            const uint8_t* wr0 = p.w + (erow + row) * KB + q * 16;
-            const uint8_t* sr0 = p.ws + (erow + row) * G;
-#pragma unroll
-            for (int h = 0; h < 2; ++h)
-              wr[c][h] = *reinterpret_cast<const u32x4*>(wr0 + (ch * kChunkGroups + 4 * h) * 16);
-            sr[c] = *reinterpret_cast<const uint2*>(sr0 + ch * kChunkGroups);
-          }
-        };
-        f32x4 acc[2][2];
-        auto clear = [&]() {
-#pragma unroll
-          for (int t = 0; t < 2; ++t)
-#pragma unroll
-            for (int c = 0; c < 2; ++c) acc[t][c] = f32x4{0.f, 0.f, 0.f, 0.f};
-        };
-        clear();
-        auto compute = [&](int ch, const u32x4 (&wr)[2][2], const uint2 (&sr)[2]) {
-#pragma unroll
-          for (int h = 0; h < 2; ++h) {
-            float sc[2];
-            bool nan[2];
-#pragma unroll
-            for (int c = 0; c < 2; ++c) {
-              const uint32_t b = ((h ? sr[c].y : sr[c].x) >> (8 * q)) & 0xFFu;
-              sc[c] = e8m0_scale(b);
-              nan[c] = b == 0xFFu;
-            }
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-              bf16x8 bfrag[2];
-#pragma unroll
-              for (int c = 0; c < 2; ++c) bfrag[c] = fp4x8_to_bf16(nan[c] ? 0u : wr[c][h][j], sc[c]);
-#pragma unroll
-              for (int t = 0; t < NT; ++t) {
-                const bf16x8 afrag = *reinterpret_cast<const bf16x8*>(
-                    &a_lds[ch][(t * 16 + c16) * kAStride + 2 * (h * 64 + j * 16 + q * 4)]);
-#pragma unroll
-                for (int c = 0; c < 2; ++c)
-                  acc[t][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(afrag, bfrag[c], acc[t][c], 0, 0, 0);
-              }
-            }
-          }
-        };
-        auto epilogue = [&](int cb) {
-#pragma unroll
-          for (int t = 0; t < NT; ++t)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              const int slot = slot_lds[t * 16 + q * 4 + i];
-              if (slot < 0) continue;
-#pragma unroll
-              for (int c = 0; c < 2; ++c) {
-                const int n = span_base + cb * kCols + 16 * c + c16;
-                if (n >= p.ncols) continue;
-                float d = round_bf16(acc[t][c][i]);
-                if (p.bias != nullptr)
-                  d = round_bf16(d + bf16_to_f32(p.bias[static_cast<int64_t>(e) * p.ncols + n]));
-                p.slot_out[static_cast<int64_t>(slot) * p.ncols + n] = d;
-              }
-            }
-          clear();
-        };
-
-        u32x4 w0[2][2], w1[2][2], w2[2][2], w3[2][2];
-        uint2 s0[2], s1[2], s2[2], s3[2];
-        load_w(0, w0, s0);
-        __builtin_amdgcn_sched_barrier(0);
-        load_w(1, w1, s1);
-        __builtin_amdgcn_sched_barrier(0);
-        load_w(2, w2, s2);
-        __builtin_amdgcn_sched_barrier(0);
-        auto step = [&](int sub, const u32x4 (&wc)[2][2], const uint2 (&sc)[2], u32x4 (&wn)[2][2],
-                        uint2 (&sn)[2]) {
-          load_w(sub + 3, wn, sn);
-          if (sub < nsub) {
-            const int cb = sub / nchunks, ch = sub - cb * nchunks;
-            compute(ch, wc, sc);
-            if (ch == nchunks - 1) epilogue(cb);
-          }
-        };
-        for (int sub = 0; sub < nsub; sub += 4) {
-          step(sub, w0, s0, w3, s3);
-          step(sub + 1, w1, s1, w0, s0);
-          step(sub + 2, w2, s2, w1, s1);
-          step(sub + 3, w3, s3, w2, s2);
-        }
-      };
-      if (ntiles == 2)
-        body(std::integral_constant<int, 2>{});
-      else
-        body(std::integral_constant<int, 1>{});
-    }
-  }
-}
-
 // Gate/up epilogue for the stream path: the projection's S fp32 partial planes
 // [S, numel, 2 ispp] are summed and finished exactly like the per-workgroup
 // epilogue above: gu = bf16(sum) (+ b13 -> bf16), g clamped from above, u on
@@ -709,29 +302,6 @@ int launch_mxfp4_stage(int stage, const void* A, int a_dtype, const uint8_t* w,
   if (numel == 0) return XK_OK;
   Mxfp4Args a{A, w, ws, bias, sorted_ids, offsets, act, slot_out, int(K), int(rows),
               int(ncols), int(numel), int(top_k), limit};
-  if (stage == 1 && (K == kChunkK || K == 2 * kChunkK) && reinterpret_cast<uintptr_t>(ws) % 8 == 0) {
-    constexpr int kSpan = 4;
-    Mxfp4V2Args v2{a, int(E)};
-    const int64_t items = E * cdiv(ncols, kSpan * 128);
-    const dim3 g2(static_cast<unsigned>(std::min<int64_t>(items, 2 * device_cu_count())));
-    hipLaunchKernelGGL((mxfp4_down_smallk<kSpan>), g2, dim3(256), 0, stream, v2);
-    XK_CHECK_LAUNCH("mxfp4_down_smallk");
-    return XK_OK;
-  }
-  if (K % kChunkK == 0 && reinterpret_cast<uintptr_t>(ws) % 8 == 0) {
-    Mxfp4V2Args v2{a, int(E)};
-    const int64_t cols = stage == 0 ? 64 : 128;
-    const int64_t items = E * cdiv(ncols, cols);
-    const dim3 g2(static_cast<unsigned>(std::min<int64_t>(items, 2 * device_cu_count())));
-    if (stage == 0 && a_dtype == XK_DT_BF16)
-      hipLaunchKernelGGL((mxfp4_stream_v2<0, uint16_t>), g2, dim3(256), 0, stream, v2);
-    else if (stage == 0)
-      hipLaunchKernelGGL((mxfp4_stream_v2<0, float>), g2, dim3(256), 0, stream, v2);
-    else
-      hipLaunchKernelGGL((mxfp4_stream_v2<1, uint16_t>), g2, dim3(256), 0, stream, v2);
-    XK_CHECK_LAUNCH("mxfp4_stream_v2");
-    return XK_OK;
-  }
   if (stage == 0) {
     const dim3 grid(static_cast<unsigned>(cdiv(ncols, 64)), static_cast<unsigned>(E));
     if (a_dtype == XK_DT_BF16)
