@@ -87,7 +87,7 @@ bool int4_use_stream(int a_dtype, int group_size, int64_t K) {
 bool int4_prefill_ok(int a_dtype, int group_size, int64_t K, int64_t N, int64_t E);
 bool int4_ksplit_ok(int64_t K, int64_t N, int64_t E, int64_t numel);
 bool int4_rs_ok(int64_t M, int64_t top_k, int64_t K, int64_t N, int64_t E);
-int rs_slices(int64_t K);
+int int4_rs_slices(int64_t K, int64_t N, int64_t numel, int64_t E);
 bool int4_rs_self_route_ok(int64_t numel);
 int launch_int4_rs(const void* A, int64_t M, int64_t K, const int32_t* packed,
                    const uint16_t* scale, int64_t E, int64_t N, int64_t numel, int64_t top_k,
@@ -138,7 +138,7 @@ Int4Kernel int4_choose(int64_t M, int64_t top_k, int64_t E, int64_t N, int64_t K
 int int4_gemm_parts(int64_t M, int64_t top_k, int64_t E, int64_t N, int64_t K, int a_dtype,
                     int group_size, int flags) {
   return int4_choose(M, top_k, E, N, K, a_dtype, group_size, flags) == Int4Kernel::kRs
-             ? rs_slices(K)
+             ? int4_rs_slices(K, N, M * top_k, E)
              : 1;
 }
 

@@ -582,11 +582,44 @@ int rs_slices(int64_t K) {
   return 0;
 }
 
+// K slices of a stream launch: as many as the LDS needs, and more (up to
+// the slice count that still divides the lines) while the work items would
+// give a wave of the grid fewer than `per_wave` column pairs, since a
+// workgroup's waves finish together only if each holds several items. The
+// estimate takes every routed slot on its own expert (at most E).
+int stream_slices(int64_t K, int64_t N, int64_t numel, int64_t E, int per_wave) {
+  int s = rs_slices(K);
+  if (s == 0) return 0;
+  const int64_t lines = K / 256, waves = int64_t(device_cu_count()) * kRsWaves;
+  const int64_t pairs = std::min(E, numel) * (N / 32);
+  while (pairs * s < per_wave * waves && lines % (2 * s) == 0) s *= 2;
+  return s;
+}
+
+#ifndef XK_MX_ITEMS_PER_WAVE
+#define XK_MX_ITEMS_PER_WAVE 8
+#endif
+#ifndef XK_RS_ITEMS_PER_WAVE
+// INT4: the LDS rule only. More slices for balance measured slower at the
+// decode shapes (C2 at 4 slices 180 vs 172 us, the N = 7168, K = 2048 down
+// projection at 2 slices 93 vs 88 us): a slice costs its activation loads
+// and partial plane more than the balance gains.
+#define XK_RS_ITEMS_PER_WAVE 0
+#endif
+
+int int4_rs_slices(int64_t K, int64_t N, int64_t numel, int64_t E) {
+  return stream_slices(K, N, numel, E, XK_RS_ITEMS_PER_WAVE);
+}
+
+int mxfp4_rs_slices(int64_t K, int64_t N, int64_t numel, int64_t E) {
+  return stream_slices(K, N, numel, E, XK_MX_ITEMS_PER_WAVE);
+}
+
 bool int4_rs_ok(int64_t M, int64_t top_k, int64_t K, int64_t N, int64_t E) {
   // the last condition: the fp32 partial planes addressable by one buffer resource
   return K % 256 == 0 && N % 32 == 0 && E <= kRsMaxE && rs_slices(K) > 0 &&
          N * (K / 8) * 4 < (int64_t(1) << 31) && M * K * 2 < (int64_t(1) << 31) &&
-         M * top_k * N * 4 * rs_slices(K) < (int64_t(1) << 31);
+         M * top_k * N * 4 * int4_rs_slices(K, N, M * top_k, E) < (int64_t(1) << 31);
 }
 
 bool int4_rs_self_route_ok(int64_t numel) { return numel <= kRsMaxSelf; }
@@ -597,29 +630,12 @@ int launch_int4_rs(const void* A, int64_t M, int64_t K, const int32_t* packed,
                    const int32_t* emap, int num_global, float* slot_out, hipStream_t stream) {
   RsArgs a{static_cast<const uint16_t*>(A), reinterpret_cast<const uint32_t*>(packed), scale,
            sorted_ids, offsets, topk_ids, emap, num_global, slot_out, int(K), int(N), int(E),
-           int(numel), int(top_k), int(top_k), rs_slices(K), static_cast<uint32_t>(M * K * 2)};
+           int(numel), int(top_k), int(top_k), int4_rs_slices(K, N, numel, E),
+           static_cast<uint32_t>(M * K * 2)};
   hipLaunchKernelGGL(int4_stream_rne, dim3(static_cast<unsigned>(device_cu_count())),
                      dim3(kRsThreads), 0, stream, a);
   XK_CHECK_LAUNCH("int4_stream_rne");
   return XK_OK;
-}
-
-#ifndef XK_MX_ITEMS_PER_WAVE
-#define XK_MX_ITEMS_PER_WAVE 8
-#endif
-
-// K slices of an MXFP4 projection: as many as the LDS needs, and more (up to
-// the slice count that still divides the lines) while the work items would
-// give a wave of the grid fewer than XK_MX_ITEMS_PER_WAVE column pairs, since
-// a workgroup's waves finish together only if each holds several items. The
-// estimate takes every routed slot on its own expert (at most E).
-int mxfp4_rs_slices(int64_t K, int64_t N, int64_t numel, int64_t E) {
-  int s = rs_slices(K);
-  if (s == 0) return 0;
-  const int64_t lines = K / 256, waves = int64_t(device_cu_count()) * kRsWaves;
-  const int64_t pairs = std::min(E, numel) * (N / 32);
-  while (pairs * s < XK_MX_ITEMS_PER_WAVE * waves && lines % (2 * s) == 0) s *= 2;
-  return s;
 }
 
 bool mxfp4_rs_ok(int64_t a_rows, int64_t K, int64_t N, int64_t E, int64_t numel) {
