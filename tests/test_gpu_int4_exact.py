@@ -98,6 +98,7 @@ def _device_inputs(M, E, N, K, ids, seed):
     (40, 6, 160, 768, 3, "zipf"),          # K / 256 odd: one-tile passes only
     (5, 4, 96, 512, 2, "uniform"),         # N not a multiple of 128
     (1024, 8, 512, 1024, 4, "zipf"),       # prefill regime: the MFMA tile kernel
+    (300, 16, 512, 512, 4, "zipf"),        # ... experts of < 128, 129-255 and > 256 rows
     (4096, 48, 4096, 7168, 8, "zipf"),     # C5 at full size, every row (tile kernel)
 ])
 def test_rows_within_fp32_summation_error(M, E, N, K, top_k, routing):
