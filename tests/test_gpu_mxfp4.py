@@ -41,8 +41,10 @@ def _ref(A, wts, ids, w, **kw):
 # hidden and ispp multiples of 256 (bf16 A): both projections run the stream
 # kernel (fp32 partial planes, SwiGLU and combine kernels); other shapes the
 # per-stage kernels
+# (600 x 8 = 4800 routed slots: more than the kernel routes itself, so the
+# align outputs feed it)
 STREAM_SHAPES = [(4, 8, 256, 256, 2), (1, 16, 512, 256, 6), (48, 32, 512, 512, 6),
-                 (33, 4, 256, 512, 2), (200, 64, 256, 256, 8)]
+                 (33, 4, 256, 512, 2), (200, 64, 256, 256, 8), (600, 32, 256, 256, 8)]
 
 
 @pytest.mark.parametrize("M,E,hidden,ispp,top_k", [(4, 8, 256, 64, 2), (1, 16, 512, 128, 6),
