@@ -14,7 +14,7 @@ The same step is also captured once into a HIP graph (``torch.cuda.CUDAGraph``,
 address-stable workspace) and replayed; its time is reported beside the eager
 one as ``ms_per_step_graph`` (``value`` stays the eager rate).
 
-    python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--no-cpu] [--fast-dequant]
+    python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--no-cpu]
     python bench.py --workload {c3-align,c3-reduce,c4,c5,f1-down,topk-softmax} [--m M]
         (secondary lines)
 """
@@ -43,8 +43,6 @@ def parse() -> argparse.Namespace:
                     help="minimum untimed warm work before each timed region (counter passes use 0)")
     ap.add_argument("--gemm-iters", type=int, default=100)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--fast-dequant", action="store_true",
-                    help="exact (n-8)*s contraction instead of the reference's bf16-rounded weights")
     ap.add_argument("--seed", type=int, default=20)
     ap.add_argument("--workload", default="c2",
                     choices=["c2", "c3-align", "c3-reduce", "c4", "c5", "f1-down", "topk-softmax"],
@@ -141,21 +139,17 @@ def time_gemm_kernel(c, flags: int, iters: int) -> float:
     return sum(d) / len(d)
 
 
-def int4_step(c, exact: bool):
-    """One fused call on the inputs ``c`` with an address-stable workspace."""
+def int4_step(c):
+    """One fused call (the public op) on the inputs ``c`` with an address-stable
+    workspace."""
     import torch
 
     from xkernels_amd import Backend, MoeInt4Workspace, fused_moe_int4_w4a16
-    from xkernels_amd.moe.hip_backend import moe_int4_w4a16_hip
 
     ws = MoeInt4Workspace.allocate(c["M"], c["top_k"], c["N"], dtype=torch.bfloat16,
                                    device="cuda", num_experts=c["E"], K=c["K"])
-    if exact:  # the public op, default (reference-rounded) dequant
-        return lambda: fused_moe_int4_w4a16(c["A"], c["packed"], c["scale"], c["ids"], c["w"],
-                                            backend=Backend.HIP, workspace=ws)
-    # the knob is a backend specialization (Impl Card knob), not a public kwarg
-    return lambda: moe_int4_w4a16_hip(c["A"], c["packed"], c["scale"], c["ids"], c["w"],
-                                      workspace=ws, exact_dequant=False)
+    return lambda: fused_moe_int4_w4a16(c["A"], c["packed"], c["scale"], c["ids"], c["w"],
+                                        backend=Backend.HIP, workspace=ws)
 
 
 def graph_time(step, steps: int, warmup: int) -> float:
@@ -192,17 +186,17 @@ def copy_calibration() -> int:
 
 
 TRAFFIC_FILE = ROOT / "profiles" / "int4_stream_rne_C2_traffic.json"
-KERNEL = {True: "int4_stream_rne", False: "int4_decode_ksplit"}  # exact dequant -> kernel name
+KERNEL = "int4_stream_rne"
 
 
-def measured_traffic(exact: bool) -> dict | None:
+def measured_traffic() -> dict | None:
     """HBM bytes per GEMM launch from the committed rocprofv3 --pmc summary
     (FETCH_SIZE and WRITE_SIZE passes, each scaled by the copy calibration)."""
     try:
         doc = json.loads(TRAFFIC_FILE.read_text())
     except (OSError, ValueError):
         return None
-    entry = doc.get("exact" if exact else "fast")
+    entry = doc.get("exact")
     return None if entry is None else entry
 
 
@@ -315,24 +309,21 @@ def secondary(a) -> dict:
                              "algorithmic_bytes": nbytes}}
     if a.workload == "f1-down":
         # the layer's down projection: N=7168 (hidden), K=2048 (intermediate), E=48
-        from xkernels_amd import _lib
-
-        exact = not a.fast_dequant
         c = make_inputs(a.seed, M=a.m, E=48, N=7168, K=2048, top_k=8)
         e_active = int(torch.unique(c["ids"]).numel())
         nbytes = int4_weight_bytes(e_active, 7168, 2048)
-        step = int4_step(c, exact)
+        step = int4_step(c)
         ms = _event_time(step, a.steps, a.warmup)
         graph_ms = graph_time(step, a.steps, a.warmup)
-        gemm_ms = time_gemm_kernel(c, 0 if exact else _lib.XK_INT4_FAST_DEQUANT, a.gemm_iters)
+        gemm_ms = time_gemm_kernel(c, 0, a.gemm_iters)
         gbs = nbytes / (ms * 1e-3) / 1e9
         kbs = nbytes / (gemm_ms * 1e-3) / 1e9
         return {"metric": f"moe_int4_w4a16 µs + HBM GB/s at M={a.m},E=48,N=7168,K=2048,top_k=8",
                 "value": round(gbs, 1), "unit": "GB/s", "higher_is_better": True,
                 "us_per_call": round(ms * 1e3, 2), "us_per_call_graph": round(graph_ms * 1e3, 2),
                 "config": {"workload": f"int4 down projection M={a.m}", "E_active": e_active,
-                           "dequant": "bf16-rounded (reference)" if exact else "exact fp32 (fast)"},
-                "roofline": {"bound": "hbm", "kernel": KERNEL[exact], "achieved": round(kbs, 1),
+                           "dequant": "bf16-rounded (reference)"},
+                "roofline": {"bound": "hbm", "kernel": KERNEL, "achieved": round(kbs, 1),
                              "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(kbs / HBM_PEAK_GBS, 4),
                              "avg_launch_us": round(gemm_ms * 1e3, 3), "algorithmic_bytes": nbytes}}
     # c5: prefill, contraction bound
@@ -412,11 +403,10 @@ def main() -> int:
             print(json.dumps(line))
         return 0
     c = make_inputs(a.seed)
-    exact = not a.fast_dequant
-    flags = 0 if exact else _lib.XK_INT4_FAST_DEQUANT
+    flags = 0
     e_active = int(torch.unique(c["ids"]).numel())
     weight_bytes = int4_weight_bytes(e_active, c["N"], c["K"])
-    step = int4_step(c, exact)
+    step = int4_step(c)
 
     if a.profile_only and a.gemm_only:
         time_gemm_kernel(c, flags, a.steps)
@@ -457,18 +447,18 @@ def main() -> int:
         "config": {"workload": "C2 int4 decode: M=64 E=48 N=4096 K=7168 top_k=8 group=32, "
                                "uniform routing, softmax weights",
                    "E_active": e_active, "weight_scale_bytes": weight_bytes,
-                   "dequant": "bf16-rounded (reference)" if exact else "exact fp32 (fast)",
+                   "dequant": "bf16-rounded (reference)",
                    "wall_s_timed_region": round(wall, 4),
                    "warm_s_before_timing": a.warm_seconds},
         "roofline": {"bound": "hbm",
-                     "kernel": KERNEL[exact],
+                     "kernel": KERNEL,
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "avg_launch_us": round(gemm_ms * 1e3, 3),
                      "algorithmic_bytes": weight_bytes,
                      "traffic": None},
     }
-    t = measured_traffic(exact)
+    t = measured_traffic()
     if t is not None:
         line["roofline"]["traffic"] = t["bytes_per_launch"]
         line["roofline"]["traffic_source"] = str(TRAFFIC_FILE.relative_to(ROOT))

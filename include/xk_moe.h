@@ -53,13 +53,9 @@ extern "C" {
 #define XK_DT_FP16 2 /* accepted by xk_moe_topk_softmax only */
 #define XK_DT_NONE (-1) /* "no tensor" for optional weights */
 
-/* int4 flags. Default (0): every dequantised weight is rounded to bf16 before
- * the contraction, as the reference does. XK_INT4_FAST_DEQUANT contracts the
- * exact (nibble-8)*scale product instead (cheaper unpack; differs from the
- * reference by the reference's own bf16 rounding of the weights) where the
- * decode K-split kernel takes the shape, and is ignored elsewhere. Other bits
- * are reserved. */
-#define XK_INT4_FAST_DEQUANT 1
+/* int4 `flags` arguments: pass 0. Every dequantised weight is rounded to bf16
+ * before the contraction, as the reference does; other values are rejected
+ * (XK_ERR_INVALID). */
 
 /* Message of the last failed call on this thread ("" if none). */
 const char* xk_last_error(void);
@@ -147,9 +143,8 @@ int xk_moe_int4_w4a16_noalloc(const void* A, int32_t a_dtype, int64_t M, int64_t
  * untouched). The decode kernel splits K: slot_out is [parts, numel, N] with
  * parts = xk_moe_int4_gemm_parts(...) for the same arguments; every plane
  * holds one K slice's partial rows and xk_moe_topk_combine(..., nparts =
- * parts) sums them. The workspace (xk_moe_int4_gemm_workspace_bytes(M, K)
- * bytes, 256-byte aligned) holds the fp16 activations XK_INT4_FAST_DEQUANT
- * prepares; other modes do not touch it and accept NULL. A, packed and scale
+ * parts) sums them. The kernels need no workspace: xk_moe_int4_gemm_workspace_bytes
+ * returns 0 and the workspace argument may be NULL. A, packed and scale
  * must be 16-byte aligned for the MFMA kernels. In the decode regime
  * (xk_moe_int4_gemm_parts(...) > 1 or M * top_k small against E, at most 4096
  * routed slots) sorted_token_ids and expert_offsets may both be NULL: the

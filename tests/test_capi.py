@@ -37,7 +37,7 @@ def test_library_exports_every_declared_symbol():
 def test_constants_match_header():
     d = _defines()
     for name in ("XK_OK", "XK_ERR_INVALID", "XK_ERR_WORKSPACE", "XK_ERR_LAUNCH", "XK_DT_BF16",
-                 "XK_DT_FP32", "XK_DT_FP16", "XK_DT_NONE", "XK_INT4_FAST_DEQUANT"):
+                 "XK_DT_FP32", "XK_DT_FP16", "XK_DT_NONE"):
         assert getattr(_lib, name) == d[name], name
     # the test-only kernel-choice bits live outside the public header
     internal = (_lib.ROOT_CSRC / "int4_flags.h").read_text()
@@ -147,11 +147,9 @@ def test_int4_gemm_stage_rejects_bad_arguments():
     assert g(K=60) == _lib.XK_ERR_INVALID
     assert g(gs=48) == _lib.XK_ERR_INVALID
     assert g(dt=3) == _lib.XK_ERR_INVALID
-    # the FAST mode's K-split kernel needs the activation workspace (K a multiple
-    # of 1024, N of 128)
-    assert g(K=1024, N=128, flags=_lib.XK_INT4_FAST_DEQUANT) == _lib.XK_ERR_WORKSPACE
-    assert g(K=1024, N=128, flags=_lib.XK_INT4_FAST_DEQUANT, ws=FAKE,
-             wsb=_lib.query("xk_moe_int4_gemm_workspace_bytes", 4, 1024) - 1) == _lib.XK_ERR_WORKSPACE
+    # flags: 0 is the only public value (the reference's bf16-rounded weights)
+    assert g(flags=1) == _lib.XK_ERR_INVALID
+    assert _lib.query("xk_moe_int4_gemm_workspace_bytes", 4, 1024) == 0
 
 
 def test_combine_rejects_bad_arguments():

@@ -21,7 +21,6 @@ from tests._helpers import assert_close, softmax_weights, uniform_topk, zipf_top
 from xkernels_amd import (Backend, MoeAlignWorkspace, MoeInt4Workspace, MoeMxfp4Workspace,
                           fused_moe_int4_w4a16, fused_moe_mxfp4, make_mxfp4_moe_weights,
                           make_w4a16_weights, moe_align_block_size)
-from xkernels_amd.moe.hip_backend import moe_int4_w4a16_hip
 
 pytestmark = pytest.mark.gpu
 REPLAYS = 4
@@ -64,9 +63,8 @@ def test_align_capture_and_replay(dev):
 
 
 @pytest.mark.parametrize("M,E,N,K,k", [(64, 48, 4096, 7168, 8), (16, 8, 1024, 2048, 2), (512, 16, 512, 1024, 4)])
-@pytest.mark.parametrize("exact", [True, False])
-def test_int4_capture_and_replay(M, E, N, K, k, exact, dev):
-    print(f"int4 graph M={M} E={E} N={N} K={K} k={k} exact={exact}", flush=True)
+def test_int4_capture_and_replay(M, E, N, K, k, dev):
+    print(f"int4 graph M={M} E={E} N={N} K={K} k={k}", flush=True)
     packed, scale, _ = make_w4a16_weights(E, N, K, 32, device=dev, seed=3, scale_hi=0.02)
     A = torch.empty(M, K, dtype=torch.bfloat16, device=dev)
     ids = torch.empty(M, k, dtype=torch.int32, device=dev)
@@ -82,10 +80,7 @@ def test_int4_capture_and_replay(M, E, N, K, k, exact, dev):
     ws = MoeInt4Workspace.allocate(M, k, N, dtype=torch.bfloat16, device=dev, num_experts=E, K=K)
 
     def call(wsp=None):
-        if exact:  # the public op
-            return fused_moe_int4_w4a16(A, packed, scale, ids, w, workspace=wsp, backend=Backend.HIP)
-        # the FAST knob is a backend specialization, not a public keyword
-        return moe_int4_w4a16_hip(A, packed, scale, ids, w, workspace=wsp, exact_dequant=False)
+        return fused_moe_int4_w4a16(A, packed, scale, ids, w, workspace=wsp, backend=Backend.HIP)
 
     graph, out = _capture(lambda: call(ws))
     assert out.data_ptr() == ws.out.data_ptr()
@@ -96,9 +91,7 @@ def test_int4_capture_and_replay(M, E, N, K, k, exact, dev):
         eager = call()
         torch.cuda.synchronize()
         assert torch.equal(out, eager), f"replay {r} differs from the eager call"
-        # the FAST knob contracts exact products, not the reference's rounded
-        # weights: its replays are checked against its own eager call only
-        if exact and r in (0, REPLAYS - 1):
+        if r in (0, REPLAYS - 1):
             assert_close(out, moe_w4a16_ref(A, packed, scale, ids, w), 2e-2, 2e-2, f"replay {r}")
 
 

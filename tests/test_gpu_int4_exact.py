@@ -12,8 +12,8 @@ oracle's bf16-rounded weights, allowing only fp32 summation error:
 (K <= 7168 terms summed in fp32 add at most about K * 2^-24 relative to the
 absolute sum; the kernels sum in groups, which is far tighter). A kernel that
 contracted the exact (n - 8) * s products instead differs by the weights'
-rounding, about 2^-9 of each term, and fails the bound: the last test checks
-that the FAST mode (exact products) is told apart.
+rounding, about 2^-9 of each term, and fails the bound: a negative control
+checks that rows computed from the exact products are told apart.
 """
 from __future__ import annotations
 
@@ -112,14 +112,20 @@ def test_rows_within_fp32_summation_error(M, E, N, K, top_k, routing):
     _bounded_check(A, packed, scale, ids, rows)
 
 
-def test_fast_mode_is_told_apart():
-    """The exact-product (FAST) rows break the bound the RNE rows meet."""
+def test_bound_tells_unrounded_weights_apart():
+    """Negative control: rows contracted over the exact (n - 8) * s products
+    (no bf16 rounding of the weights) break the bound the kernels' rows meet."""
     if not torch.cuda.is_available():
         pytest.skip("no GPU")
     M, E, N, K, top_k = 64, 48, 4096, 7168, 8
     ids = uniform_topk(M, top_k, E, 3)
     A, packed, scale, ids = _device_inputs(M, E, N, K, ids, 11)
-    rows = _gemm_rows(A, packed, scale, ids, flags=_lib.XK_INT4_FAST_DEQUANT)
+    flat = ids.reshape(-1).long()
+    rows = torch.empty(M * top_k, N, dtype=torch.float64, device=A.device)
+    for e in flat.unique().tolist():
+        slots = (flat == e).nonzero().reshape(-1)
+        W = dequant_w4a16(packed[e:e + 1], scale[e:e + 1], 32, out_dtype=torch.float32)[0].double()
+        rows[slots] = A[slots // top_k].double() @ W.T
     with pytest.raises(AssertionError, match="fp32-summation bound"):
         _bounded_check(A, packed, scale, ids, rows)
 

