@@ -7,9 +7,11 @@
 // Decode experts hold ~11 routed rows, so every packed weight byte feeds one
 // 16-row MFMA tile and the kernel is a weight stream (792 MB at the headline
 // shape) with ~2.1 VALU instructions of exact dequant per weight. Measured on
-// MI355X, VALU work and the HBM stream of a CU do not overlap (their times
-// add, even when they run in different waves), so the design removes every
-// other cost from the stream and keeps the dequant at its minimum:
+// MI355X, that VALU hides only partly under the stream (at the headline shape:
+// loads alone 139 us, the whole kernel 171-176 us, a plain read of the same
+// bytes ~128 us), so the design removes every other cost from the stream and
+// keeps the dequant at its minimum. The same stream serves MXFP4 weights
+// (mxfp4_stream_rs below):
 //   * work item = (expert, 16-row pass, K slice, 32 output columns). K is cut
 //     into S slices only as far as one slice of the pass's activations fits
 //     the LDS (S = 2 at K = 7168); every slice writes its own fp32 partial
