@@ -97,7 +97,8 @@ def warm(fn, steps: int) -> None:
 
 
 def time_gemm_kernel(c, flags: int, iters: int) -> float:
-    """Average duration (ms) of one grouped-GEMM launch, HIP events on its stream."""
+    """Average duration (ms) of one grouped-GEMM launch: HIP events on its stream
+    around ``iters`` back-to-back launches."""
     import torch
 
     from xkernels_amd import _lib
@@ -128,15 +129,16 @@ def time_gemm_kernel(c, flags: int, iters: int) -> float:
                   flags, gws.data_ptr(), gws.numel(), s)
 
     warm(launch, 10)
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(iters)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(iters)]
-    for i in range(iters):
-        starts[i].record(stream)
+    # one event pair around the back-to-back launches: an event pair around
+    # every launch adds ~3 us of event overhead to each (an empty kernel of this
+    # launch shape measures 6.0 us that way, 2.9 us back to back)
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record(stream)
+    for _ in range(iters):
         launch()
-        ends[i].record(stream)
+    ev1.record(stream)
     torch.cuda.synchronize()
-    d = sorted(a.elapsed_time(b) for a, b in zip(starts, ends))
-    return sum(d) / len(d)
+    return ev0.elapsed_time(ev1) / iters
 
 
 def int4_step(c):
