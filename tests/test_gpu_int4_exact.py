@@ -94,7 +94,8 @@ def _device_inputs(M, E, N, K, ids, seed):
     (64, 48, 7168, 2048, 8, "uniform"),    # the down projection of the same layer
     (16, 48, 7168, 2048, 8, "uniform"),    # ... at M = 16 and M = 1
     (1, 48, 7168, 2048, 8, "uniform"),
-    (192, 16, 512, 1024, 4, "zipf"),       # experts with several 32-row passes
+    (96, 16, 512, 1024, 4, "zipf"),        # experts with several 16-row passes (stream kernel)
+    (192, 16, 512, 1024, 4, "zipf"),       # 48 rows per expert: the tile kernel
     (40, 6, 160, 768, 3, "zipf"),          # K / 256 odd: one-tile passes only
     (5, 4, 96, 512, 2, "uniform"),         # N not a multiple of 128
     (1024, 8, 512, 1024, 4, "zipf"),       # prefill regime: the MFMA tile kernel
@@ -132,7 +133,7 @@ def test_bound_tells_unrounded_weights_apart():
 
 @pytest.mark.parametrize("M,E,N,K,top_k,routing,ep", [
     (64, 48, 4096, 7168, 8, "uniform", False),  # C2
-    (192, 16, 512, 1024, 4, "zipf", False),     # several 16-row passes per expert
+    (96, 16, 512, 1024, 4, "zipf", False),      # several 16-row passes per expert
     (64, 48, 7168, 2048, 8, "zipf", True),      # expert map: half the experts local
     (1, 48, 4096, 7168, 8, "uniform", False),
 ])
