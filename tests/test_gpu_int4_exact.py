@@ -97,6 +97,10 @@ def _device_inputs(M, E, N, K, ids, seed):
     (96, 16, 512, 1024, 4, "zipf"),        # experts with several 16-row passes (stream kernel)
     (192, 16, 512, 1024, 4, "zipf"),       # 48 rows per expert: the tile kernel
     (40, 6, 160, 768, 3, "zipf"),          # K / 256 odd: one-tile passes only
+    (64, 48, 2880, 2880, 8, "uniform"),    # K % 256 != 0: the last 256-k line zero-padded
+    (1, 16, 256, 320, 4, "uniform"),       # ... 64 k in the last line
+    (200, 8, 256, 1344, 4, "zipf"),        # ... experts with several 16-row passes
+    (16, 8, 512, 2080, 2, "zipf"),         # K % 64 != 0: the scalar kernel
     (5, 4, 96, 512, 2, "uniform"),         # N not a multiple of 128
     (1024, 8, 512, 1024, 4, "zipf"),       # prefill regime: the MFMA tile kernel
     (300, 16, 512, 512, 4, "zipf"),        # ... experts of < 128, 129-255 and > 256 rows

@@ -38,15 +38,16 @@ def _ref(A, wts, ids, w, **kw):
     return moe_mxfp4_ref(A, *(wts[k] for k in KEYS), ids, w, b13=wts["b13"], b2=wts["b2"], **kw)
 
 
-# hidden and ispp multiples of 256 (bf16 A) and fewer than 20 routed rows per
-# expert on average: both projections run the stream kernel (fp32 partial
-# planes, SwiGLU and combine kernels); other shapes the per-stage kernels.
+# bf16 A and fewer than 20 routed rows per expert on average: both projections
+# run the stream kernel (fp32 partial planes, SwiGLU and combine kernels);
+# other shapes the per-stage kernels. Hidden 384 / ispp 640: K not a multiple
+# of 256 (but of 128), the last 256-k line zero-padded.
 # 600 x 8 = 4800 routed slots on 256 experts: more than the stream kernel
 # routes itself, so the align outputs feed it; 200 x 8 on 64 experts (25 rows
 # per expert) runs the per-stage kernels.
 STREAM_SHAPES = [(4, 8, 256, 256, 2), (1, 16, 512, 256, 6), (48, 32, 512, 512, 6),
                  (33, 4, 256, 512, 2), (100, 64, 256, 256, 8), (600, 256, 256, 256, 8),
-                 (200, 64, 256, 256, 8)]
+                 (200, 64, 256, 256, 8), (8, 16, 384, 640, 4)]
 
 
 @pytest.mark.parametrize("M,E,hidden,ispp,top_k", [(4, 8, 256, 64, 2), (1, 16, 512, 128, 6),

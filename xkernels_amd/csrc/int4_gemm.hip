@@ -78,7 +78,7 @@ int int4_block_size() { return 16; }
 
 // The MFMA kernels take bf16 activations with 32-wide quantisation groups.
 bool int4_use_stream(int a_dtype, int group_size, int64_t K) {
-  return a_dtype == XK_DT_BF16 && group_size == 32 && K % 256 == 0;
+  return a_dtype == XK_DT_BF16 && group_size == 32 && K % 64 == 0;
 }
 
 bool int4_prefill_ok(int a_dtype, int group_size, int64_t K, int64_t N, int64_t E);

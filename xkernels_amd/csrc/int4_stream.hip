@@ -192,7 +192,12 @@ __device__ __forceinline__ f32x4 quad_transpose(f32x4 e) {
   return e;
 }
 
-template <int FMT>
+// PADK: K is not a multiple of 256 (the last line zero-padded). The scale
+// rows are then not 16-byte multiples, so the block-start scale loads are
+// 4-byte loads: each lies wholly inside or wholly past the buffer (a 16-byte
+// load that straddles the end of the scales comes back empty, real bytes
+// included), and needs only 4-byte alignment of the rows.
+template <int FMT, bool PADK>
 __device__ __forceinline__ void stream_body(const RsArgs& p) {
   using F = RsFmt<FMT>;
   constexpr int SB = F::kScaleBytes;
@@ -207,7 +212,8 @@ __device__ __forceinline__ void stream_body(const RsArgs& p) {
   const int wave = uniform(tid >> 6);
   const int c16 = lane & 15, q = lane >> 4;
   const int K = p.K, N = p.N, E = p.E, G = K >> 5, KW = K >> 3;
-  const int S = p.slices, Ks = K / S, nl = Ks >> 8;
+  // K is cut into 256-k lines, the last one zero-padded when K % 256 != 0
+  const int S = p.slices, nl = ((K + 255) >> 8) / S, Ks = nl << 8;
   const bool paired = XK_RS_PAIRED && S > 1 && gridDim.x % (8 * S) == 0;
   const int ncp = N >> 5;            // column pairs per expert
   const int nblk = nl * 8;           // 1 KiB operand blocks of one activation slice
@@ -309,6 +315,19 @@ __device__ __forceinline__ void stream_body(const RsArgs& p) {
     }
     XK_WAIT_VMCNT(0);
     lds_sync();
+    if constexpr (PADK) {
+      if (s * Ks + Ks > K) {
+        // the slice runs past K: its activations there are zero (the weights
+        // and scales the stream reads there are finite: other columns' data,
+        // or zero past the buffer), after every wave's loads have landed
+        for (int t = tid; t < nblk * 64; t += kRsThreads) {
+          const int blk = t >> 6, qq = (t & 63) >> 4;
+          const int j = blk & 3, h = (blk >> 2) & 1, line = blk >> 3;
+          if (s * Ks + line * 256 + (4 * h + qq) * 32 + 8 * j >= K) a_lds[t] = u32x4{0u, 0u, 0u, 0u};
+        }
+        lds_sync();
+      }
+    }
   };
 
   // One chunk: this wave's `cnt` column pairs from `my_lo` of expert e,
@@ -381,9 +400,18 @@ __device__ __forceinline__ void stream_body(const RsArgs& p) {
         if (blk) {  // lanes past the slice's last line read nothing (offset past the buffer)
 #pragma unroll
           for (int i = 0; i < F::kScLoads; ++i)
-            sl.s[c][i] = __builtin_amdgcn_raw_buffer_load_b128(
-                rs, pl + (q + 4 * i) * F::kLinesPerLoad < nl ? s_lane + 16 * (q + 4 * i) : (1 << 30),
-                so + c * 16 * G * SB, XK_RS_LOAD_POLICY);
+          {
+            const int voff = pl + (q + 4 * i) * F::kLinesPerLoad < nl ? s_lane + 16 * (q + 4 * i) : (1 << 30);
+            if constexpr (PADK) {
+#pragma unroll
+              for (int d = 0; d < 4; ++d)
+                sl.s[c][i][d] = __builtin_amdgcn_raw_buffer_load_b32(rs, voff + 4 * d, so + c * 16 * G * SB,
+                                                                     XK_RS_LOAD_POLICY);
+            } else {
+              sl.s[c][i] = __builtin_amdgcn_raw_buffer_load_b128(rs, voff, so + c * 16 * G * SB,
+                                                                 XK_RS_LOAD_POLICY);
+            }
+          }
         }
       }
       // advance (value selects keep the cursor in scalar registers)
@@ -558,7 +586,14 @@ __device__ __forceinline__ void stream_body(const RsArgs& p) {
 __global__ void __launch_bounds__(kRsThreads)
 __attribute__((amdgpu_waves_per_eu(kRsWaves / 4, kRsWaves / 4)))
 int4_stream_rne(RsArgs p) {
-  stream_body<kFmtInt4>(p);
+  stream_body<kFmtInt4, false>(p);
+}
+
+// K not a multiple of 256 (a multiple of 64: 4-byte scale rows).
+__global__ void __launch_bounds__(kRsThreads)
+__attribute__((amdgpu_waves_per_eu(kRsWaves / 4, kRsWaves / 4)))
+int4_stream_rne_padk(RsArgs p) {
+  stream_body<kFmtInt4, true>(p);
 }
 
 // The same stream over MXFP4 weights (e2m1 nibbles, one e8m0 scale byte per
@@ -569,18 +604,26 @@ int4_stream_rne(RsArgs p) {
 __global__ void __launch_bounds__(kRsThreads)
 __attribute__((amdgpu_waves_per_eu(kRsWaves / 4, kRsWaves / 4)))
 mxfp4_stream_rs(RsArgs p) {
-  stream_body<kFmtFp4>(p);
+  stream_body<kFmtFp4, false>(p);
+}
+
+// K not a multiple of 256 (a multiple of 128: 4-byte scale rows).
+__global__ void __launch_bounds__(kRsThreads)
+__attribute__((amdgpu_waves_per_eu(kRsWaves / 4, kRsWaves / 4)))
+mxfp4_stream_rs_padk(RsArgs p) {
+  stream_body<kFmtFp4, true>(p);
 }
 
 }  // namespace
 
-// K slices for one 16-row pass: the fewest (K / 256 split evenly) whose
-// activation block fits the LDS buffer.
+// K slices for one 16-row pass: the fewest (the ceil(K / 256) lines split
+// evenly) whose activation block fits the LDS buffer. K must be a multiple of
+// the 32-element group.
 int rs_slices(int64_t K) {
-  if (K % 256 != 0) return 0;
-  const int64_t lines = K / 256;
+  if (K % 32 != 0 || K <= 0) return 0;
+  const int64_t lines = (K + 255) / 256;  // the last one zero-padded
   for (int64_t s = 1; s <= lines; ++s)
-    if (lines % s == 0 && 16 * (K / s) * 2 <= kRsLdsA) return static_cast<int>(s);
+    if (lines % s == 0 && 16 * (lines / s) * 256 * 2 <= kRsLdsA) return static_cast<int>(s);
   return 0;
 }
 
@@ -592,7 +635,7 @@ int rs_slices(int64_t K) {
 int stream_slices(int64_t K, int64_t N, int64_t numel, int64_t E, int per_wave) {
   int s = rs_slices(K);
   if (s == 0) return 0;
-  const int64_t lines = K / 256, waves = int64_t(device_cu_count()) * kRsWaves;
+  const int64_t lines = (K + 255) / 256, waves = int64_t(device_cu_count()) * kRsWaves;
   const int64_t pairs = std::min(E, numel) * (N / 32);
   while (pairs * s < per_wave * waves && lines % (2 * s) == 0) s *= 2;
   return s;
@@ -619,7 +662,8 @@ int mxfp4_rs_slices(int64_t K, int64_t N, int64_t numel, int64_t E) {
 
 bool int4_rs_ok(int64_t M, int64_t top_k, int64_t K, int64_t N, int64_t E) {
   // the last condition: the fp32 partial planes addressable by one buffer resource
-  return K % 256 == 0 && N % 32 == 0 && E <= kRsMaxE && rs_slices(K) > 0 &&
+  // K % 64: 4-byte aligned scale rows for the padded variant
+  return K % 64 == 0 && N % 32 == 0 && E <= kRsMaxE && rs_slices(K) > 0 &&
          N * (K / 8) * 4 < (int64_t(1) << 31) && M * K * 2 < (int64_t(1) << 31) &&
          M * top_k * N * 4 * int4_rs_slices(K, N, M * top_k, E) < (int64_t(1) << 31);
 }
@@ -634,14 +678,18 @@ int launch_int4_rs(const void* A, int64_t M, int64_t K, const int32_t* packed,
            sorted_ids, offsets, topk_ids, emap, num_global, slot_out, int(K), int(N), int(E),
            int(numel), int(top_k), int(top_k), int4_rs_slices(K, N, numel, E),
            static_cast<uint32_t>(M * K * 2)};
-  hipLaunchKernelGGL(int4_stream_rne, dim3(static_cast<unsigned>(device_cu_count())),
-                     dim3(kRsThreads), 0, stream, a);
+  if (K % 256 == 0)
+    hipLaunchKernelGGL(int4_stream_rne, dim3(static_cast<unsigned>(device_cu_count())),
+                       dim3(kRsThreads), 0, stream, a);
+  else
+    hipLaunchKernelGGL(int4_stream_rne_padk, dim3(static_cast<unsigned>(device_cu_count())),
+                       dim3(kRsThreads), 0, stream, a);
   XK_CHECK_LAUNCH("int4_stream_rne");
   return XK_OK;
 }
 
 bool mxfp4_rs_ok(int64_t a_rows, int64_t K, int64_t N, int64_t E, int64_t numel) {
-  const int s = K % 256 == 0 ? mxfp4_rs_slices(K, N, numel, E) : 0;
+  const int s = K % 128 == 0 ? mxfp4_rs_slices(K, N, numel, E) : 0;  // 4-byte scale rows
   return s > 0 && N % 32 == 0 && E <= kRsMaxE && N * (K / 2) < (int64_t(1) << 31) &&
          a_rows * K * 2 < (int64_t(1) << 31) && numel * N * 4 * s < (int64_t(1) << 31);
 }
@@ -653,8 +701,12 @@ int launch_mxfp4_rs(const void* A, int64_t a_rows, int64_t K, const uint8_t* w, 
   RsArgs a{static_cast<const uint16_t*>(A), reinterpret_cast<const uint32_t*>(w), ws, sorted_ids,
            offsets, topk_ids, emap, num_global, planes, int(K), int(N), int(E), int(numel), 1,
            int(a_row_div), mxfp4_rs_slices(K, N, numel, E), static_cast<uint32_t>(a_rows * K * 2)};
-  hipLaunchKernelGGL(mxfp4_stream_rs, dim3(static_cast<unsigned>(device_cu_count())),
-                     dim3(kRsThreads), 0, stream, a);
+  if (K % 256 == 0)
+    hipLaunchKernelGGL(mxfp4_stream_rs, dim3(static_cast<unsigned>(device_cu_count())),
+                       dim3(kRsThreads), 0, stream, a);
+  else
+    hipLaunchKernelGGL(mxfp4_stream_rs_padk, dim3(static_cast<unsigned>(device_cu_count())),
+                       dim3(kRsThreads), 0, stream, a);
   XK_CHECK_LAUNCH("mxfp4_stream_rs");
   return XK_OK;
 }
