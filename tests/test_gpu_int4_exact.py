@@ -101,6 +101,7 @@ def _device_inputs(M, E, N, K, ids, seed):
     (1, 16, 256, 320, 4, "uniform"),       # ... 64 k in the last line
     (200, 8, 256, 1344, 4, "zipf"),        # ... experts with several 16-row passes
     (16, 8, 512, 2080, 2, "zipf"),         # K % 64 != 0: the scalar kernel
+    (16, 384, 256, 512, 8, "uniform"),     # 384 local experts (the stream kernel takes up to 512)
     (5, 4, 96, 512, 2, "uniform"),         # N not a multiple of 128
     (1024, 8, 512, 1024, 4, "zipf"),       # prefill regime: the MFMA tile kernel
     (300, 16, 512, 512, 4, "zipf"),        # ... experts of < 128, 129-255 and > 256 rows

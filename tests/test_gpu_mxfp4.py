@@ -47,7 +47,7 @@ def _ref(A, wts, ids, w, **kw):
 # per expert) runs the per-stage kernels.
 STREAM_SHAPES = [(4, 8, 256, 256, 2), (1, 16, 512, 256, 6), (48, 32, 512, 512, 6),
                  (33, 4, 256, 512, 2), (100, 64, 256, 256, 8), (600, 256, 256, 256, 8),
-                 (200, 64, 256, 256, 8), (8, 16, 384, 640, 4)]
+                 (200, 64, 256, 256, 8), (8, 16, 384, 640, 4), (8, 384, 256, 256, 6)]
 
 
 @pytest.mark.parametrize("M,E,hidden,ispp,top_k", [(4, 8, 256, 64, 2), (1, 16, 512, 128, 6),

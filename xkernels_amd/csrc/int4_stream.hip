@@ -103,7 +103,7 @@ template <int FMT> struct RsFmt {
 };
 constexpr int kRsRing = XK_RS_RING;         // ring slots: lines k+1 .. k+R-1 in flight while line k computes
 constexpr int kRsLdsA = 112 * 1024;         // bytes of LDS for one activation slice
-constexpr int kRsMaxE = 256;
+constexpr int kRsMaxE = 512;
 constexpr int kRsMaxSelf = 4096;            // routed slots a workgroup can route for itself
 
 struct RsArgs {

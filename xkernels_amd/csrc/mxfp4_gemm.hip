@@ -8,7 +8,7 @@
 // followed by the weighted top-k combine (reduce.hip). The bf16 roundings sit
 // where the reference's bf16 torch ops round (matmul output, bias add, act).
 //
-// Main path (bf16 activations, hidden and ispp multiples of 128, E <= 256):
+// Main path (bf16 activations, hidden and ispp multiples of 128, E <= 512):
 // both projections run mxfp4_stream_rs (int4_stream.hip) into fp32 partial
 // planes; mxfp4_swiglu_planes below finishes stage 0 and the combine applies
 // stage 1's roundings and bias. Every other shape runs mxfp4_stream_gemm: a
