@@ -47,7 +47,8 @@ def test_bf16_matches_oracle(M, E, N, K, top_k, mul_routed, dev):
     assert_close(got, want, 2e-2, 2e-2, "int4 bf16")
 
 
-@pytest.mark.parametrize("M,E,N,K,top_k", [(16, 4, 32, 64, 2), (5, 8, 64, 256, 3)])
+@pytest.mark.parametrize("M,E,N,K,top_k", [(16, 4, 32, 64, 2), (5, 8, 64, 256, 3), (16, 16, 1024, 2048, 4),
+                                           (64, 48, 200, 288, 8), (33, 4, 128, 256, 4)])
 def test_fp32_matches_oracle(M, E, N, K, top_k, dev):
     A, packed, scale, ids, w = _case(M, E, N, K, top_k, dtype=torch.float32)
     got = _run(A, packed, scale, ids, w, dev)
@@ -122,6 +123,16 @@ def test_config2_decode_full_size(dev):
     got = fused_moe_int4_w4a16(A, packed, scale, ids, w, backend=Backend.HIP)
     want = moe_w4a16_ref(A, packed, scale, ids, w)  # oracle evaluated on the device copy
     assert_close(got, want, 2e-2, 2e-2, "C2")
+
+
+def test_config2_fp32_activations_full_size(dev):
+    """C2 shapes with fp32 activations and an fp32 output (spec tolerance 1e-3)."""
+    ids = uniform_topk(64, 8, 48, 21)
+    A, packed, scale, ids, w = _device_case(64, 48, 4096, 7168, 8, ids, 20)
+    A = torch.randn(64, 7168, generator=torch.Generator(device="cuda").manual_seed(23), device="cuda")
+    got = fused_moe_int4_w4a16(A, packed, scale, ids, w, backend=Backend.HIP)
+    assert got.dtype == torch.float32
+    assert_close(got, moe_w4a16_ref(A, packed, scale, ids, w), 1e-3, 1e-3, "C2 fp32")
 
 
 def test_config5_prefill_full_size(dev):

@@ -37,6 +37,7 @@ def _gemm_rows(A, packed, scale, ids, flags=0, self_route=False, emap=None):
     top_k = ids.shape[1]
     numel = M * top_k
     dev = A.device
+    dt = _lib.XK_DT_FP32 if A.dtype == torch.float32 else _lib.XK_DT_BF16
     bs = _lib.query("xk_moe_int4_block_size", M, top_k, E)
     max_pad = numel + (E + 1) * (bs - 1)
     sorted_ids = torch.empty(max_pad, dtype=torch.int32, device=dev)
@@ -51,11 +52,11 @@ def _gemm_rows(A, packed, scale, ids, flags=0, self_route=False, emap=None):
     _lib.call("xk_moe_align_block_size", ids.data_ptr(), numel, E, bs, ep, ng, sorted_ids.data_ptr(),
               expert_ids.data_ptr(), num_post.data_ptr(), offsets.data_ptr(), aws.data_ptr(),
               aws.numel(), s)
-    parts = _lib.query("xk_moe_int4_gemm_parts", M, top_k, E, N, K, _lib.XK_DT_BF16, 32, flags)
+    parts = _lib.query("xk_moe_int4_gemm_parts", M, top_k, E, N, K, dt, 32, flags)
     out = torch.full((parts, numel, N), float("nan"), dtype=torch.float32, device=dev)
     gws = torch.empty(max(256, _lib.query("xk_moe_int4_gemm_workspace_bytes", M, K)), dtype=torch.uint8,
                       device=dev)
-    _lib.call("xk_moe_int4_w4a16_gemm", A.data_ptr(), _lib.XK_DT_BF16, M, K, packed.data_ptr(),
+    _lib.call("xk_moe_int4_w4a16_gemm", A.data_ptr(), dt, M, K, packed.data_ptr(),
               scale.data_ptr(), E, N, 32, ids.data_ptr(), top_k, ep, ng,
               None if self_route else sorted_ids.data_ptr(), None if self_route else offsets.data_ptr(),
               out.data_ptr(), flags, gws.data_ptr(), gws.numel(), s)
@@ -63,17 +64,23 @@ def _gemm_rows(A, packed, scale, ids, flags=0, self_route=False, emap=None):
     return out.sum(0)
 
 
-def _bounded_check(A, packed, scale, ids, rows):
-    """Compares every routed slot's row, one expert at a time (float64 reference)."""
+def _bounded_check(A, packed, scale, ids, rows, rel=REL, w_dtype=torch.bfloat16, emap=None):
+    """Compares every routed slot's row, one expert at a time (float64 reference
+    over the weights dequantised to ``w_dtype``: bf16-rounded for bf16
+    activations, the exact fp32 products for fp32 ones)."""
     top_k = ids.shape[1]
     flat = ids.reshape(-1).long()
+    if emap is not None:
+        flat = emap.long()[flat]
     worst = 0.0
     for e in flat.unique().tolist():
+        if e < 0:
+            continue
         slots = (flat == e).nonzero().reshape(-1)
-        W = dequant_w4a16(packed[e:e + 1], scale[e:e + 1], 32, out_dtype=torch.bfloat16)[0].double()
+        W = dequant_w4a16(packed[e:e + 1], scale[e:e + 1], 32, out_dtype=w_dtype)[0].double()
         a = A[slots // top_k].double()
         want = a @ W.T
-        bound = REL * (a.abs() @ W.abs().T) + 1e-30
+        bound = rel * (a.abs() @ W.abs().T) + 1e-30
         err = (rows[slots].double() - want).abs()
         ratio = float((err / bound).max())
         worst = max(worst, ratio)
@@ -164,3 +171,71 @@ def test_self_routed_rows_equal_aligned_rows(M, E, N, K, top_k, routing, ep):
     if ep:
         local = (ids.reshape(-1) >= E // 2)
         assert not torch.isnan(routed[local]).any() and torch.isnan(routed[~local]).all()
+
+
+# fp32 activations: the reference contracts them with the exact (n - 8) * s
+# products in fp32 (w4a16.py:21-50 dequantises to the activation dtype). The
+# MFMA stream kernel splits both operands into bf16 pairs (the weight split is
+# exact, the activation split leaves 2^-17 of |a|) and drops the lo * lo
+# product (2^-18 of |a w|), so every row is within 2^-15 of sum |a w|; a
+# kernel that rounded the activations to bf16 (2^-9 of each term) fails it.
+REL_F32 = 2.0 ** -15
+
+
+@pytest.mark.parametrize("M,E,N,K,top_k,routing", [
+    (64, 48, 4096, 7168, 8, "uniform"),    # C2 shape with fp32 activations
+    (16, 8, 1024, 2048, 2, "uniform"),     # C1 shape
+    (96, 16, 512, 1024, 4, "zipf"),        # experts with several 16-row passes
+    (1024, 8, 512, 1024, 4, "zipf"),       # prefill regime: fp32 stays on the stream kernel
+    (64, 48, 2880, 2880, 8, "uniform"),    # K % 256 != 0: the padded variant
+    (1, 16, 256, 320, 4, "uniform"),
+    (16, 8, 512, 2080, 2, "zipf"),         # K % 64 != 0: the scalar kernel
+    (16, 384, 256, 512, 8, "uniform"),     # 384 local experts
+])
+def test_fp32_rows_within_split_error(M, E, N, K, top_k, routing):
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    ids = uniform_topk(M, top_k, E, 3) if routing == "uniform" else zipf_topk(M, top_k, E, 1.2, 3)
+    print(f"fp32 case M={M} E={E} N={N} K={K} top_k={top_k} {routing}", flush=True)
+    A, packed, scale, ids = _device_inputs(M, E, N, K, ids, 11)
+    g = torch.Generator(device="cuda").manual_seed(17)
+    A = torch.randn(M, K, generator=g, device="cuda")  # full fp32 mantissas
+    rows = _gemm_rows(A, packed, scale, ids)
+    assert not torch.isnan(rows).any(), "a routed slot's row was not written"
+    _bounded_check(A, packed, scale, ids, rows, rel=REL_F32, w_dtype=torch.float32)
+
+
+def test_fp32_bound_tells_bf16_activations_apart():
+    """Negative control: the same kernel fed the activations rounded to bf16
+    breaks the fp32 bound against the unrounded activations."""
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    M, E, N, K, top_k = 16, 8, 1024, 2048, 2
+    ids = uniform_topk(M, top_k, E, 3)
+    _, packed, scale, ids = _device_inputs(M, E, N, K, ids, 11)
+    A = torch.randn(M, K, generator=torch.Generator(device="cuda").manual_seed(17), device="cuda")
+    rows = _gemm_rows(A.to(torch.bfloat16).float(), packed, scale, ids)
+    with pytest.raises(AssertionError, match="fp32-summation bound"):
+        _bounded_check(A, packed, scale, ids, rows, rel=REL_F32, w_dtype=torch.float32)
+
+
+@pytest.mark.parametrize("M,E,N,K,top_k,ep", [(64, 48, 4096, 7168, 8, False), (64, 48, 7168, 2048, 8, True)])
+def test_fp32_self_routed_rows_equal_aligned_rows(M, E, N, K, top_k, ep):
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    print(f"fp32 self-route M={M} E={E} N={N} K={K} k={top_k} ep={ep}", flush=True)
+    ids = zipf_topk(M, top_k, E, 1.2, 5)
+    _, packed, scale, ids = _device_inputs(M, E, N, K, ids, 13)
+    A = torch.randn(M, K, generator=torch.Generator(device="cuda").manual_seed(19), device="cuda")
+    emap = None
+    if ep:
+        E_loc = E // 2
+        emap = torch.full((E,), -1, dtype=torch.int32, device="cuda")
+        emap[E_loc:] = torch.arange(E_loc, dtype=torch.int32, device="cuda")
+        packed, scale = packed[E_loc:].contiguous(), scale[E_loc:].contiguous()
+    aligned = _gemm_rows(A, packed, scale, ids, emap=emap)
+    routed = _gemm_rows(A, packed, scale, ids, emap=emap, self_route=True)
+    assert torch.equal(torch.isnan(aligned), torch.isnan(routed))
+    assert torch.equal(torch.nan_to_num(aligned), torch.nan_to_num(routed))
+    _bounded_check(A, packed, scale, ids, torch.nan_to_num(routed), rel=REL_F32, w_dtype=torch.float32,
+                   emap=emap)

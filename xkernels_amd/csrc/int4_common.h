@@ -66,6 +66,41 @@ __device__ __forceinline__ bf16x8 dequant_rne_nat(uint32_t w, const RneScale& k,
   return __builtin_bit_cast(bf16x8, b);
 }
 
+// dequant_rne_nat's exact fp32 products (n - 8) s as a bf16 pair hi + lo ==
+// (n - 8) s exactly: hi rounds the product to nearest even, lo is the
+// remainder (the product has at most 12 significant bits, so the remainder
+// has at most 5 and is exact in bf16). For fp32 activations, whose reference
+// contraction uses the unrounded products.
+__device__ __forceinline__ void dequant_split_nat(uint32_t w, const RneScale& k, uint32_t mlo,
+                                                  uint32_t mhi, bf16x8& hi, bf16x8& lo) {
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  typedef float f2 __attribute__((ext_vector_type(2)));
+  typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+  const uint32_t w8 = w >> 8;
+  const h2 x[4] = {__builtin_bit_cast(h2, and_or(w, mlo, 0x64006400u)),
+                   __builtin_bit_cast(h2, and_or(w, mhi, 0x54005400u)),
+                   __builtin_bit_cast(h2, and_or(w8, mlo, 0x64006400u)),
+                   __builtin_bit_cast(h2, and_or(w8, mhi, 0x54005400u))};
+  float v[8];
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    const float c = (d & 1) ? k.m72 : k.m1032;
+    v[d] = fmaf(static_cast<float>(x[d][0]), k.s, c);
+    v[d + 4] = fmaf(static_cast<float>(x[d][1]), k.s, c);
+  }
+  u32x4 bh, bl;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const uint32_t h = __builtin_bit_cast(uint32_t, __builtin_convertvector((f2{v[2 * e], v[2 * e + 1]}), b2));
+    const float r0 = v[2 * e] - __uint_as_float(h << 16);
+    const float r1 = v[2 * e + 1] - __uint_as_float(h & 0xFFFF0000u);
+    bh[e] = h;
+    bl[e] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f2{r0, r1}), b2));
+  }
+  hi = __builtin_bit_cast(bf16x8, bh);
+  lo = __builtin_bit_cast(bf16x8, bl);
+}
+
 // e8m0 byte -> the scale operand of v_cvt_scalef32_pk_bf16_fp4, which applies
 // only the exponent field of its f32 operand: the byte placed there gives
 // 2^(b-127), byte 0 included (2^-127, as in the reference). Byte 0xFF (the

@@ -76,16 +76,17 @@ int device_cu_count() {
 // Token-slot block size the MFMA kernels consume (one MFMA row tile).
 int int4_block_size() { return 16; }
 
-// The MFMA kernels take bf16 activations with 32-wide quantisation groups.
+// The MFMA kernels take 32-wide quantisation groups and bf16 activations
+// (fp32 activations: the weight-streaming kernel only).
 bool int4_use_stream(int a_dtype, int group_size, int64_t K) {
-  return a_dtype == XK_DT_BF16 && group_size == 32 && K % 64 == 0;
+  return (a_dtype == XK_DT_BF16 || a_dtype == XK_DT_FP32) && group_size == 32 && K % 64 == 0;
 }
 
 bool int4_prefill_ok(int a_dtype, int group_size, int64_t K, int64_t N, int64_t E);
-bool int4_rs_ok(int64_t M, int64_t top_k, int64_t K, int64_t N, int64_t E);
-int int4_rs_slices(int64_t K, int64_t N, int64_t numel, int64_t E);
+bool int4_rs_ok(int64_t M, int64_t top_k, int64_t K, int64_t N, int64_t E, bool f32a);
+int int4_rs_slices(int64_t K, int64_t N, int64_t numel, int64_t E, bool f32a);
 bool int4_rs_self_route_ok(int64_t numel);
-int launch_int4_rs(const void* A, int64_t M, int64_t K, const int32_t* packed,
+int launch_int4_rs(const void* A, bool f32a, int64_t M, int64_t K, const int32_t* packed,
                    const uint16_t* scale, int64_t E, int64_t N, int64_t numel, int64_t top_k,
                    const int32_t* sorted_ids, const int32_t* offsets, const int32_t* topk_ids,
                    const int32_t* emap, int num_global, float* slot_out, hipStream_t stream);
@@ -118,8 +119,9 @@ Int4Kernel int4_choose(int64_t M, int64_t top_k, int64_t E, int64_t N, int64_t K
                        int group_size, int flags) {
   if (!int4_use_stream(a_dtype, group_size, K)) return Int4Kernel::kSimple;
   const int64_t numel = M * top_k;
-  const bool tile_ok = int4_prefill_ok(a_dtype, group_size, K, N, E);
-  const bool rs_ok = int4_rs_ok(M, top_k, K, N, E);
+  const bool f32a = a_dtype == XK_DT_FP32;
+  const bool tile_ok = !f32a && int4_prefill_ok(a_dtype, group_size, K, N, E);
+  const bool rs_ok = int4_rs_ok(M, top_k, K, N, E, f32a);
   bool tile = tile_ok && numel >= kPrefillRowsPerExpert * E;
   if (flags & XK_INT4_TEST_FORCE_TILE) tile = tile_ok;
   if (flags & XK_INT4_TEST_FORCE_STREAM) tile = tile && !rs_ok;
@@ -133,7 +135,7 @@ Int4Kernel int4_choose(int64_t M, int64_t top_k, int64_t E, int64_t N, int64_t K
 int int4_gemm_parts(int64_t M, int64_t top_k, int64_t E, int64_t N, int64_t K, int a_dtype,
                     int group_size, int flags) {
   return int4_choose(M, top_k, E, N, K, a_dtype, group_size, flags) == Int4Kernel::kRs
-             ? int4_rs_slices(K, N, M * top_k, E)
+             ? int4_rs_slices(K, N, M * top_k, E, a_dtype == XK_DT_FP32)
              : 1;
 }
 
@@ -181,7 +183,7 @@ int launch_int4_gemm(const void* A, int a_dtype, int64_t M, int64_t K, const int
       return launch_int4_prefill(A, K, packed, scale, E, N, numel, top_k, sorted_ids, offsets,
                                  slot_out, stream);
     case Int4Kernel::kRs:
-      return launch_int4_rs(A, M, K, packed, scale, E, N, numel, top_k, sorted_ids, offsets,
+      return launch_int4_rs(A, a_dtype == XK_DT_FP32, M, K, packed, scale, E, N, numel, top_k, sorted_ids, offsets,
                             topk_ids, emap, num_global, slot_out, stream);
     case Int4Kernel::kSimple:
       break;

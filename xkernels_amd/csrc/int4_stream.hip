@@ -197,7 +197,14 @@ __device__ __forceinline__ f32x4 quad_transpose(f32x4 e) {
 // 4-byte loads: each lies wholly inside or wholly past the buffer (a 16-byte
 // load that straddles the end of the scales comes back empty, real bytes
 // included), and needs only 4-byte alignment of the rows.
-template <int FMT, bool PADK>
+// F32A (INT4 only): fp32 activations, whose reference contraction uses the
+// exact products (n - 8) s. The activations are staged as a bf16 pair hi + lo
+// (A - hi - lo <= 2^-16 |A|), the weights split exactly (dequant_split_nat),
+// and three MFMAs per fragment add hi*hi + hi*lo + lo*hi (lo*lo is below
+// 2^-16 of the product): about 2^-15 relative error per term, against the
+// spec's fp32 tolerance of 1e-3. The two activation planes halve the K a
+// slice holds.
+template <int FMT, bool PADK, bool F32A = false>
 __device__ __forceinline__ void stream_body(const RsArgs& p) {
   using F = RsFmt<FMT>;
   constexpr int SB = F::kScaleBytes;
@@ -305,6 +312,36 @@ __device__ __forceinline__ void stream_body(const RsArgs& p) {
       }
       const int t = p.sorted_ids[row0 + c16];
       sid = t < p.numel ? t : -1;
+    }
+    if constexpr (F32A) {
+      lds_sync();  // the row table is complete
+      const float* A32 = reinterpret_cast<const float*>(p.A);
+      for (int t = tid; t < nblk * 64; t += kRsThreads) {
+        const int blk = t >> 6, ln = t & 63, qq = ln >> 4;
+        const int j = blk & 3, h = (blk >> 2) & 1, line = blk >> 3;
+        const int k0 = s * Ks + line * 256 + (4 * h + qq) * 32 + 8 * j;
+        const int slot = row_slot[ln & 15];
+        u32x4 vh = u32x4{0u, 0u, 0u, 0u}, vl = vh;
+        if (slot >= 0 && k0 < K) {
+          const float* a = A32 + static_cast<int64_t>(slot / p.a_row_div) * K + k0;
+          const f32x4 x0 = *reinterpret_cast<const f32x4*>(a), x1 = *reinterpret_cast<const f32x4*>(a + 4);
+          const float x[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+#pragma unroll
+          for (int e2 = 0; e2 < 4; ++e2) {
+            typedef float f2 __attribute__((ext_vector_type(2)));
+            typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+            const uint32_t hh = __builtin_bit_cast(uint32_t, __builtin_convertvector((f2{x[2 * e2], x[2 * e2 + 1]}), b2));
+            const float r0 = x[2 * e2] - __uint_as_float(hh << 16);
+            const float r1 = x[2 * e2 + 1] - __uint_as_float(hh & 0xFFFF0000u);
+            vh[e2] = hh;
+            vl[e2] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f2{r0, r1}), b2));
+          }
+        }
+        a_lds[t] = vh;
+        a_lds[nblk * 64 + t] = vl;
+      }
+      lds_sync();
+      return;
     }
     // rows of pad slots read nothing (an offset past A; their LDS rows only
     // feed output rows that are never stored)
@@ -465,12 +502,15 @@ __device__ __forceinline__ void stream_body(const RsArgs& p) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           bf16x8 bfrag[2];
+          [[maybe_unused]] bf16x8 blo[2];
 #pragma unroll
           for (int c = 0; c < 2; ++c) {
 #if XK_RS_VARIANT == 3
             bfrag[c] = __builtin_bit_cast(bf16x8, sl.w[c][h]);
 #else
-            if constexpr (FMT == kFmtInt4)
+            if constexpr (F32A)
+              dequant_split_nat(sl.w[c][h][j], ks[c], kNibMask, kNibMaskHi, bfrag[c], blo[c]);
+            else if constexpr (FMT == kFmtInt4)
               bfrag[c] = dequant_rne_nat(sl.w[c][h][j], ks[c], kNibMask, kNibMaskHi);
             else
               bfrag[c] = fp4x8_to_bf16(fnan[c] ? 0u : sl.w[c][h][j], fs[c]);
@@ -484,9 +524,19 @@ __device__ __forceinline__ void stream_body(const RsArgs& p) {
           }
 #else
           const bf16x8 afrag = __builtin_bit_cast(bf16x8, a_lds[lbase + (h * 4 + j) * 64]);
+          if constexpr (F32A) {
+            const bf16x8 alo = __builtin_bit_cast(bf16x8, a_lds[nblk * 64 + lbase + (h * 4 + j) * 64]);
 #pragma unroll
-          for (int c = 0; c < 2; ++c)
-            acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(afrag, bfrag[c], acc[c], 0, 0, 0);
+            for (int c = 0; c < 2; ++c) {
+              acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(afrag, bfrag[c], acc[c], 0, 0, 0);
+              acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(afrag, blo[c], acc[c], 0, 0, 0);
+              acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(alo, bfrag[c], acc[c], 0, 0, 0);
+            }
+          } else {
+#pragma unroll
+            for (int c = 0; c < 2; ++c)
+              acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(afrag, bfrag[c], acc[c], 0, 0, 0);
+          }
 #endif
         }
       }
@@ -596,6 +646,19 @@ int4_stream_rne_padk(RsArgs p) {
   stream_body<kFmtInt4, true>(p);
 }
 
+// fp32 activations (K a multiple of 256, and the padded variant).
+__global__ void __launch_bounds__(kRsThreads)
+__attribute__((amdgpu_waves_per_eu(kRsWaves / 4, kRsWaves / 4)))
+int4_stream_rne_f32(RsArgs p) {
+  stream_body<kFmtInt4, false, true>(p);
+}
+
+__global__ void __launch_bounds__(kRsThreads)
+__attribute__((amdgpu_waves_per_eu(kRsWaves / 4, kRsWaves / 4)))
+int4_stream_rne_f32_padk(RsArgs p) {
+  stream_body<kFmtInt4, true, true>(p);
+}
+
 // The same stream over MXFP4 weights (e2m1 nibbles, one e8m0 scale byte per
 // 32-element group: 2^(b - 127), byte 0xFF read as 0): each 8-nibble word
 // becomes 8 bf16 with four v_cvt_scalef32_pk_bf16_fp4 (exact: an e2m1 value
@@ -617,13 +680,14 @@ mxfp4_stream_rs_padk(RsArgs p) {
 }  // namespace
 
 // K slices for one 16-row pass: the fewest (the ceil(K / 256) lines split
-// evenly) whose activation block fits the LDS buffer. K must be a multiple of
-// the 32-element group.
-int rs_slices(int64_t K) {
+// evenly) whose activation block fits the LDS buffer (two bf16 planes for
+// fp32 activations). K must be a multiple of the 32-element group.
+int rs_slices(int64_t K, bool f32a) {
   if (K % 32 != 0 || K <= 0) return 0;
   const int64_t lines = (K + 255) / 256;  // the last one zero-padded
+  const int64_t bytes = f32a ? 4 : 2;
   for (int64_t s = 1; s <= lines; ++s)
-    if (lines % s == 0 && 16 * (lines / s) * 256 * 2 <= kRsLdsA) return static_cast<int>(s);
+    if (lines % s == 0 && 16 * (lines / s) * 256 * bytes <= kRsLdsA) return static_cast<int>(s);
   return 0;
 }
 
@@ -632,8 +696,8 @@ int rs_slices(int64_t K) {
 // give a wave of the grid fewer than `per_wave` column pairs, since a
 // workgroup's waves finish together only if each holds several items. The
 // estimate takes every routed slot on its own expert (at most E).
-int stream_slices(int64_t K, int64_t N, int64_t numel, int64_t E, int per_wave) {
-  int s = rs_slices(K);
+int stream_slices(int64_t K, int64_t N, int64_t numel, int64_t E, int per_wave, bool f32a) {
+  int s = rs_slices(K, f32a);
   if (s == 0) return 0;
   const int64_t lines = (K + 255) / 256, waves = int64_t(device_cu_count()) * kRsWaves;
   const int64_t pairs = std::min(E, numel) * (N / 32);
@@ -652,38 +716,40 @@ int stream_slices(int64_t K, int64_t N, int64_t numel, int64_t E, int per_wave) 
 #define XK_RS_ITEMS_PER_WAVE 0
 #endif
 
-int int4_rs_slices(int64_t K, int64_t N, int64_t numel, int64_t E) {
-  return stream_slices(K, N, numel, E, XK_RS_ITEMS_PER_WAVE);
+int int4_rs_slices(int64_t K, int64_t N, int64_t numel, int64_t E, bool f32a) {
+  return stream_slices(K, N, numel, E, XK_RS_ITEMS_PER_WAVE, f32a);
 }
 
 int mxfp4_rs_slices(int64_t K, int64_t N, int64_t numel, int64_t E) {
-  return stream_slices(K, N, numel, E, XK_MX_ITEMS_PER_WAVE);
+  return stream_slices(K, N, numel, E, XK_MX_ITEMS_PER_WAVE, false);
 }
 
-bool int4_rs_ok(int64_t M, int64_t top_k, int64_t K, int64_t N, int64_t E) {
+bool int4_rs_ok(int64_t M, int64_t top_k, int64_t K, int64_t N, int64_t E, bool f32a) {
   // the last condition: the fp32 partial planes addressable by one buffer resource
   // K % 64: 4-byte aligned scale rows for the padded variant
-  return K % 64 == 0 && N % 32 == 0 && E <= kRsMaxE && rs_slices(K) > 0 &&
-         N * (K / 8) * 4 < (int64_t(1) << 31) && M * K * 2 < (int64_t(1) << 31) &&
-         M * top_k * N * 4 * int4_rs_slices(K, N, M * top_k, E) < (int64_t(1) << 31);
+  return K % 64 == 0 && N % 32 == 0 && E <= kRsMaxE && rs_slices(K, f32a) > 0 &&
+         N * (K / 8) * 4 < (int64_t(1) << 31) && M * K * 4 < (int64_t(1) << 31) &&
+         M * top_k * N * 4 * int4_rs_slices(K, N, M * top_k, E, f32a) < (int64_t(1) << 31);
 }
 
 bool int4_rs_self_route_ok(int64_t numel) { return numel <= kRsMaxSelf; }
 
-int launch_int4_rs(const void* A, int64_t M, int64_t K, const int32_t* packed,
+int launch_int4_rs(const void* A, bool f32a, int64_t M, int64_t K, const int32_t* packed,
                    const uint16_t* scale, int64_t E, int64_t N, int64_t numel, int64_t top_k,
                    const int32_t* sorted_ids, const int32_t* offsets, const int32_t* topk_ids,
                    const int32_t* emap, int num_global, float* slot_out, hipStream_t stream) {
   RsArgs a{static_cast<const uint16_t*>(A), reinterpret_cast<const uint32_t*>(packed), scale,
            sorted_ids, offsets, topk_ids, emap, num_global, slot_out, int(K), int(N), int(E),
-           int(numel), int(top_k), int(top_k), int4_rs_slices(K, N, numel, E),
-           static_cast<uint32_t>(M * K * 2)};
-  if (K % 256 == 0)
-    hipLaunchKernelGGL(int4_stream_rne, dim3(static_cast<unsigned>(device_cu_count())),
+           int(numel), int(top_k), int(top_k), int4_rs_slices(K, N, numel, E, f32a),
+           static_cast<uint32_t>(M * K * (f32a ? 4 : 2))};
+  const dim3 grid(static_cast<unsigned>(device_cu_count()));
+  const bool padk = K % 256 != 0;
+  if (f32a)
+    hipLaunchKernelGGL(padk ? int4_stream_rne_f32_padk : int4_stream_rne_f32, grid,
                        dim3(kRsThreads), 0, stream, a);
   else
-    hipLaunchKernelGGL(int4_stream_rne_padk, dim3(static_cast<unsigned>(device_cu_count())),
-                       dim3(kRsThreads), 0, stream, a);
+    hipLaunchKernelGGL(padk ? int4_stream_rne_padk : int4_stream_rne, grid, dim3(kRsThreads), 0,
+                       stream, a);
   XK_CHECK_LAUNCH("int4_stream_rne");
   return XK_OK;
 }
