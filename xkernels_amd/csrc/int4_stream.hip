@@ -204,6 +204,15 @@ __device__ __forceinline__ f32x4 quad_transpose(f32x4 e) {
 // 2^-16 of the product): about 2^-15 relative error per term, against the
 // spec's fp32 tolerance of 1e-3. The two activation planes halve the K a
 // slice holds.
+#if XK_RS_TIMELINE
+// diagnostic builds: per-workgroup phase timestamps (s_memrealtime, 100 MHz)
+// of the last launch per K: [K == 4096 ? 0 : 1][block][phase]
+__device__ unsigned long long xk_tl[2][256][6];
+__device__ unsigned long long xk_tlw[2][256][16];
+#define XK_TL(ph) do { if (threadIdx.x == 0 && blockIdx.x < 256) xk_tl[p.K == 4096 ? 0 : 1][blockIdx.x][ph] = __builtin_amdgcn_s_memrealtime(); } while (0)
+#else
+#define XK_TL(ph) do { } while (0)
+#endif
 template <int FMT, bool PADK, bool F32A = false>
 __device__ __forceinline__ void stream_body(const RsArgs& p) {
   using F = RsFmt<FMT>;
@@ -214,9 +223,13 @@ __device__ __forceinline__ void stream_body(const RsArgs& p) {
   __shared__ int cnt[kRsMaxE];
   __shared__ int16_t slot_expert[kRsMaxSelf];
   __shared__ u32x4 sc_lds[kRsWaves][2][kRsScLines * 16];  // per wave: a block of group scales
+  __shared__ int left_lds[kRsWaves];  // INT4: steps each wave has left
+  int left = 0;
 
+  XK_TL(0);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = uniform(tid >> 6);
+
   const int c16 = lane & 15, q = lane >> 4;
   const int K = p.K, N = p.N, E = p.E, G = K >> 5, KW = K >> 3;
   // K is cut into 256-k lines, the last one zero-padded when K % 256 != 0
@@ -265,6 +278,7 @@ __device__ __forceinline__ void stream_body(const RsArgs& p) {
   // scales that straddle a slice boundary (a column's scale row is K / 16
   // bytes, not a multiple of 128) are fetched once for both. Otherwise the
   // items (expert, pass, slice, column pair) are split evenly.
+  XK_TL(1);
   const int total_items = uniform(pref[E]);
   const int b = blockIdx.x;
   const int gsz = paired ? static_cast<int>(gridDim.x) / S : static_cast<int>(gridDim.x);
@@ -582,6 +596,15 @@ __device__ __forceinline__ void stream_body(const RsArgs& p) {
       cl = tend ? 0 : cl1;
       ci += tend ? 1 : 0;
       ++cst;
+      if constexpr (FMT == kFmtInt4) {
+        // the wave with more steps left than its SIMD partner issues first
+        left_lds[wave] = --left;
+        const int other = __builtin_amdgcn_readfirstlane(left_lds[wave ^ 4]);
+        if (other < left)
+          __builtin_amdgcn_s_setprio(1);
+        else
+          __builtin_amdgcn_s_setprio(0);
+      }
     };
     for (int st = 0; st < padded; st += kRsRing)
       static_for<kRsRing>([&](auto d) { step(d); });
@@ -592,6 +615,38 @@ __device__ __forceinline__ void stream_body(const RsArgs& p) {
 
   // Walk this workgroup's item range: segments of one (expert, pass, slice),
   // cut into chunks of at most kRsWaves * kRsMaxCp column pairs.
+  // INT4: the two waves of a SIMD (w and w ^ 4) finish together when the
+  // one with more steps left gets the issue priority; without it the older
+  // wave wins the arbitration and the younger one runs its last pairs alone
+  // (C2 per-wave end times 114 vs 144 us; GEMM 166.5 -> 161.8 us). Each wave
+  // first counts the steps of its share (the same walk as below, no loads).
+  if constexpr (FMT == kFmtInt4) {
+    int rot2 = 0, pos2 = item_beg;
+    while (pos2 < item_end) {
+      int lo = 0, hi = E;
+      while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (pref[mid] <= pos2) lo = mid; else hi = mid;
+      }
+      const int e = uniform(lo);
+      const int local = pos2 - pref[e];
+      const int cp0 = local % ncp;
+      const int cpe = min(ncp, cp0 + (item_end - pos2));
+      for (int c0 = cp0; c0 < cpe; c0 += kRsWaves * kRsMaxCp) {
+        const int lc = min(kRsWaves * kRsMaxCp, cpe - c0);
+        const int base = lc / kRsWaves, rem = lc % kRsWaves;
+        const int r = (wave - rot2 + kRsWaves) % kRsWaves;
+        const int cnt = base + (r < rem ? 1 : 0);
+        if (cnt > 0) left += (cnt * nl + kRsRing - 1) / kRsRing * kRsRing;
+        rot2 = (rot2 + rem) % kRsWaves;
+      }
+      pos2 += cpe - cp0;
+    }
+    left_lds[wave] = left;  // read after the first segment's barrier
+#if XK_RS_TIMELINE
+    if (lane == 0 && blockIdx.x < 256) xk_tlw[p.K == 4096 ? 0 : 1][blockIdx.x][8 + wave] = left;
+#endif
+  }
   int loaded = -1;  // first item of the segment whose activations are in LDS
   int rot = 0;      // first wave to take a remainder pair in the next chunk
   int pos = item_beg;
@@ -609,6 +664,7 @@ __device__ __forceinline__ void stream_body(const RsArgs& p) {
     const int seg_id = uniform(pos - cp0);
     if (seg_id != loaded) {
       load_segment(e, pass, s);
+      if (loaded < 0) XK_TL(2);
       loaded = seg_id;
     }
     for (int c0 = cp0; c0 < cpe; c0 += kRsWaves * kRsMaxCp) {
@@ -630,7 +686,15 @@ __device__ __forceinline__ void stream_body(const RsArgs& p) {
     }
     pos += cpe - cp0;
   }
+  XK_TL(3);
+#if XK_RS_TIMELINE
+  if (lane == 0 && blockIdx.x < 256) xk_tlw[p.K == 4096 ? 0 : 1][blockIdx.x][wave] = __builtin_amdgcn_s_memrealtime();
+#endif
   write_kept();
+#if XK_RS_TIMELINE
+  __syncthreads();
+#endif
+  XK_TL(4);
 }
 
 __global__ void __launch_bounds__(kRsThreads)
@@ -778,3 +842,11 @@ int launch_mxfp4_rs(const void* A, int64_t a_rows, int64_t K, const uint8_t* w, 
 }
 
 }  // namespace xk
+
+#if XK_RS_TIMELINE
+extern "C" int xk_debug_timeline(void* host) {
+  if (hipMemcpyFromSymbol(host, HIP_SYMBOL(xk::xk_tl), sizeof(xk::xk_tl)) != hipSuccess) return 1;
+  return hipMemcpyFromSymbol(static_cast<char*>(host) + sizeof(xk::xk_tl), HIP_SYMBOL(xk::xk_tlw),
+                             sizeof(xk::xk_tlw)) == hipSuccess ? 0 : 1;
+}
+#endif
