@@ -599,7 +599,7 @@ __device__ __forceinline__ void stream_body(const RsArgs& p) {
       if constexpr (FMT == kFmtInt4) {
         // the wave with more steps left than its SIMD partner issues first
         left_lds[wave] = --left;
-        const int other = __builtin_amdgcn_readfirstlane(left_lds[wave ^ 4]);
+        const int other = __builtin_amdgcn_readfirstlane(left_lds[(wave + 4) % kRsWaves]);
         if (other < left)
           __builtin_amdgcn_s_setprio(1);
         else
