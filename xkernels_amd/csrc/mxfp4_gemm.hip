@@ -257,9 +257,25 @@ mxfp4_swiglu_planes(const float* __restrict__ planes, int S, int64_t numel, int 
   if (e < 0) return;
   const int64_t pstride = numel * 2 * ispp;
   const float* row = planes + t * 2 * ispp;
+  // the planes in groups of four loads in flight (a decode batch of one token
+  // has 16 K slices: 9.5 -> 6.8 us; groups of eight measured 12.2 us)
   f32x4 g = *reinterpret_cast<const f32x4*>(row + j0);
   f32x4 u = *reinterpret_cast<const f32x4*>(row + ispp + j0);
-  for (int sl = 1; sl < S; ++sl) {
+  int sl = 1;
+  for (; sl + 3 < S; sl += 4) {
+    f32x4 gs[4], us[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      gs[i] = *reinterpret_cast<const f32x4*>(row + (sl + i) * pstride + j0);
+      us[i] = *reinterpret_cast<const f32x4*>(row + (sl + i) * pstride + ispp + j0);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      g += gs[i];
+      u += us[i];
+    }
+  }
+  for (; sl < S; ++sl) {
     g += *reinterpret_cast<const f32x4*>(row + sl * pstride + j0);
     u += *reinterpret_cast<const f32x4*>(row + sl * pstride + ispp + j0);
   }
