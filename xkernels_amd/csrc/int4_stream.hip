@@ -8,7 +8,7 @@
 // 16-row MFMA tile and the kernel is a weight stream (792 MB at the headline
 // shape) with ~2.1 VALU instructions of exact dequant per weight. Measured on
 // MI355X, that VALU hides only partly under the stream (at the headline shape:
-// loads alone 139 us, the whole kernel 171-176 us, a plain read of the same
+// loads alone 139 us, the whole kernel 164-168 us, a plain read of the same
 // bytes ~128 us), so the design removes every other cost from the stream and
 // keeps the dequant at its minimum. The same stream serves MXFP4 weights
 // (mxfp4_stream_rs below):
@@ -27,7 +27,8 @@
 //     slots are not read;
 //   * each wave streams its column pairs with no barrier: a ring of lines
 //     (4 x 16-byte weight loads per 128-byte line of 32 columns) in flight,
-//     one line dequantised and contracted per step;
+//     one line dequantised and contracted per step; the two waves of a SIMD
+//     trade issue priority by the steps each has left, so they end together;
 //   * group scales come in 8-line blocks: on a block's first line, four loads
 //     read 128 contiguous bytes of every column (lane (c, q): lines + q and
 //     + q + 4), the wave parks them in a private 4 KiB LDS area and each step
@@ -47,7 +48,9 @@
 //     kRsMaxSelf routed slots) every workgroup routes for itself: the mapped
 //     expert of every slot goes to LDS with a histogram (LDS atomics), and a
 //     segment's 16 rows are found by one wave's ballot scan of that list. The
-//     rows of an expert then follow ascending slot order, like the align.
+//     rows of an expert then follow ascending slot order, like the align;
+//   * fp32 activations (INT4): staged as bf16 pairs hi + lo through registers,
+//     weights split exactly into bf16 hi + lo, three MFMAs per fragment.
 #include "int4_common.h"
 
 #ifndef XK_RS_VARIANT
