@@ -239,3 +239,61 @@ def test_fp32_self_routed_rows_equal_aligned_rows(M, E, N, K, top_k, ep):
     assert torch.equal(torch.nan_to_num(aligned), torch.nan_to_num(routed))
     _bounded_check(A, packed, scale, ids, torch.nan_to_num(routed), rel=REL_F32, w_dtype=torch.float32,
                    emap=emap)
+
+
+def _sweep_cases(n=24, seed=2026):
+    """Seeded random shapes over the kernels' eligibility boundaries: K a
+    multiple of 64 (stream kernel; K % 256 != 0 takes the padded variant), N a
+    multiple of 32, 1..64 and a few hundred experts, 1..300 tokens (stream and
+    tile kernels), bf16 and fp32 activations, align-fed or self-routed, with or
+    without an expert map."""
+    import random
+    rng = random.Random(seed)
+    cases = []
+    for i in range(n):
+        E = rng.choice([2, 3, 5, 8, 16, 33, 48, 64, 200])
+        top_k = rng.randint(1, min(8, E))
+        cases.append(dict(M=rng.choice([1, 2, 7, 16, 37, 64, 130, 300]), E=E,
+                          N=32 * rng.randint(1, 32), K=64 * rng.randint(1, 48), top_k=top_k,
+                          routing=rng.choice(["uniform", "zipf"]),
+                          fp32=rng.random() < 0.3, self_route=rng.random() < 0.5,
+                          ep=rng.random() < 0.25, seed=100 + i))
+    return cases
+
+
+@pytest.mark.parametrize("case", _sweep_cases(), ids=lambda c: "M{M}-E{E}-N{N}-K{K}-k{top_k}".format(**c))
+def test_random_shapes_within_bound(case):
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    c = case
+    print(f"sweep {c}", flush=True)
+    M, E, N, K, top_k = c["M"], c["E"], c["N"], c["K"], c["top_k"]
+    ids = (uniform_topk(M, top_k, E, c["seed"]) if c["routing"] == "uniform"
+           else zipf_topk(M, top_k, E, 1.2, c["seed"]))
+    A, packed, scale, ids = _device_inputs(M, E, N, K, ids, c["seed"])
+    if c["fp32"]:
+        A = torch.randn(M, K, generator=torch.Generator(device="cuda").manual_seed(c["seed"]), device="cuda")
+    emap = None
+    if c["ep"] and E >= 2:
+        E_loc = E // 2
+        emap = torch.full((E,), -1, dtype=torch.int32, device="cuda")
+        emap[E - E_loc:] = torch.arange(E_loc, dtype=torch.int32, device="cuda")
+        packed, scale = packed[E - E_loc:].contiguous(), scale[E - E_loc:].contiguous()
+    # without align outputs only the decode kernel runs (it routes for itself);
+    # the others refuse the call
+    rows = None
+    if c["self_route"]:
+        try:
+            rows = _gemm_rows(A, packed, scale, ids, emap=emap, self_route=True)
+        except RuntimeError as err:
+            assert "align outputs" in str(err), err
+    if rows is None:
+        rows = _gemm_rows(A, packed, scale, ids, emap=emap)
+    flat = ids.reshape(-1).long()
+    local = torch.ones_like(flat, dtype=torch.bool) if emap is None else emap.long()[flat] >= 0
+    assert not torch.isnan(rows[local]).any(), "a routed local slot's row was not written"
+    if c["fp32"]:
+        _bounded_check(A, packed, scale, ids, torch.nan_to_num(rows), rel=REL_F32, w_dtype=torch.float32,
+                       emap=emap)
+    else:
+        _bounded_check(A, packed, scale, ids, torch.nan_to_num(rows), emap=emap)

@@ -191,3 +191,33 @@ def test_known_answer_clamp_and_bias(dev):
     out = fused_moe_mxfp4(x["A"], *(x[k] for k in KEYS), x["topk_ids"], x["topk_w"], b13=x["b13"],
                           b2=x["b2"], swiglu_limit=x["swiglu_limit"], backend=Backend.HIP)
     kat.check(out)
+
+
+def _sweep_cases(n=16, seed=2027):
+    """Seeded random shapes: hidden and ispp multiples of 128 (stream kernels,
+    the last 256-k line zero-padded when not a multiple of 256) or of 32 (the
+    per-stage kernels), 1..300 tokens on 2..300 experts, bias and SwiGLU limit
+    on or off."""
+    import random
+    rng = random.Random(seed)
+    cases = []
+    for i in range(n):
+        unit = rng.choice([128, 128, 32])
+        E = rng.choice([2, 5, 16, 64, 130, 300])
+        cases.append(dict(M=rng.choice([1, 3, 16, 48, 100, 300]), E=E,
+                          hidden=unit * rng.randint(1, 8), ispp=unit * rng.randint(1, 6),
+                          top_k=rng.randint(1, min(8, E)), bias=rng.random() < 0.5,
+                          limit=rng.choice([None, 7.0]), seed=200 + i))
+    return cases
+
+
+@pytest.mark.parametrize("case", _sweep_cases(),
+                         ids=lambda c: "M{M}-E{E}-h{hidden}-i{ispp}-k{top_k}".format(**c))
+def test_random_shapes_match_oracle(case, dev):
+    c = case
+    print(f"sweep {c}", flush=True)
+    A, wts, ids, w = _case(c["M"], c["E"], c["hidden"], c["ispp"], c["top_k"], bias=c["bias"],
+                           seed=c["seed"])
+    A = (A.float() * 0.1).to(A.dtype)
+    got = _run(A, wts, ids, w, dev, swiglu_limit=c["limit"])
+    assert_close(got, _ref(A, wts, ids, w, swiglu_limit=c["limit"]), 2e-2, 2e-2, "mxfp4 sweep")
