@@ -120,7 +120,7 @@ def test_tile_kernel_unweighted_and_expert_parallel(dev):
 
 
 def test_default_choice_uses_tile_kernel_at_prefill_sizes(dev):
-    """numel >= 30 E selects the tile kernel by default; its result equals the
+    """numel >= 17 E selects the tile kernel by default; its result equals the
     forced tile kernel's bit for bit."""
     M, E, N, K, k = 1024, 16, 512, 512, 4
     ids = zipf_topk(M, k, E, 1.2, 5)

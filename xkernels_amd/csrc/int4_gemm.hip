@@ -10,7 +10,7 @@
 // weighted top-k combine runs afterwards (reduce.hip). Kernels:
 //   * int4_stream_rne (int4_stream.hip): decode regime, bf16 A, group 32 —
 //     weight streaming with the exact bf16 dequant, K-slice partial planes;
-//   * int4_prefill_tile (int4_prefill.hip): prefill regime (>= 30 routed rows
+//   * int4_prefill_tile (int4_prefill.hip): prefill regime (>= 17 routed rows
 //     per expert on average), MFMA tiles, the same exact dequant;
 //   * int4_simple_gemm (below): any dtype, group size or shape the MFMA
 //     kernels do not take — one thread per (slot, column), exact dequant
@@ -97,10 +97,10 @@ int launch_int4_prefill(const void* A, int64_t K, const int32_t* packed, const u
 
 // Routed rows per expert (on average) from which the tile kernel replaces the
 // weight-streaming kernel, which streams every expert's weights once per
-// 16-row pass. Measured at E = 48, N = 4096, K = 7168, top_k = 8: stream vs
-// tile 352.5 vs 360.4 us at 29.3 rows per expert, 362.5 vs 351.6 us at 32,
-// 477 vs 366 us at 42.7.
-constexpr int64_t kPrefillRowsPerExpert = 30;
+// 16-row pass. Measured at E = 48, N = 4096, K = 7168, top_k = 8 (uniform
+// routing): stream vs tile 177.2 vs 248.4 us at 13.3 rows per expert, 228.9
+// vs 248.1 us at 16, 264.4 vs 249.8 us at 18.7, 294.6 vs 249.2 us at 21.3.
+constexpr int64_t kPrefillRowsPerExpert = 17;
 
 // The INT4 kernels need no workspace; the argument and this size stay in the
 // interface (0 bytes, NULL accepted).
