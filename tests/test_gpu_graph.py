@@ -95,6 +95,36 @@ def test_int4_capture_and_replay(M, E, N, K, k, dev):
             assert_close(out, moe_w4a16_ref(A, packed, scale, ids, w), 2e-2, 2e-2, f"replay {r}")
 
 
+def test_int4_fp32_activations_capture_and_replay(dev):
+    """fp32 activations (the stream kernel's split-bf16 variant) captured and
+    replayed with new inputs, equal to the eager call every time."""
+    M, E, N, K, k = 64, 48, 4096, 7168, 8
+    packed, scale, _ = make_w4a16_weights(E, N, K, 32, device=dev, seed=4, scale_hi=0.02)
+    A = torch.empty(M, K, dtype=torch.float32, device=dev)
+    ids = torch.empty(M, k, dtype=torch.int32, device=dev)
+    w = torch.empty(M, k, dtype=torch.float32, device=dev)
+
+    def load(seed):
+        g = torch.Generator(device=dev).manual_seed(seed)
+        A.copy_(torch.randn(M, K, generator=g, device=dev))
+        ids.copy_(uniform_topk(M, k, E, seed).to(dev))
+        w.copy_(softmax_weights(M, k, seed).to(dev))
+
+    load(1)
+    ws = MoeInt4Workspace.allocate(M, k, N, dtype=torch.float32, device=dev, num_experts=E, K=K)
+    call = lambda wsp=None: fused_moe_int4_w4a16(A, packed, scale, ids, w, workspace=wsp,  # noqa: E731
+                                                 backend=Backend.HIP)
+    graph, out = _capture(lambda: call(ws))
+    for r in range(REPLAYS):
+        print(f"int4 fp32 replay {r}", flush=True)
+        load(300 + r)
+        graph.replay()
+        eager = call()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {r} differs from the eager call"
+    assert_close(out, moe_w4a16_ref(A, packed, scale, ids, w), 1e-3, 1e-3, "fp32 replay")
+
+
 def test_mxfp4_capture_and_replay(dev):
     M, E, hidden, ispp, k = 48, 32, 512, 128, 6
     wts = make_mxfp4_moe_weights(E, hidden, ispp, with_bias=True, device=dev, seed=5)

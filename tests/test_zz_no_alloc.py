@@ -24,14 +24,15 @@ def _inputs(M, E, N, K, k, seed, routing="uniform"):
 def _args(A, packed, scale, ids, w, flags):
     M, K = A.shape
     E, N, _ = packed.shape
-    return [A.data_ptr(), _lib.XK_DT_BF16, M, K, packed.data_ptr(), scale.data_ptr(), E, N, 32,
+    dt = _lib.XK_DT_FP32 if A.dtype == torch.float32 else _lib.XK_DT_BF16
+    return [A.data_ptr(), dt, M, K, packed.data_ptr(), scale.data_ptr(), E, N, 32,
             ids.data_ptr(), w.data_ptr(), ids.shape[1], None, 0, 1, flags]
 
 
 def _with_workspace(A, packed, scale, ids, w, flags=0):
     M, K = A.shape
     E, N, _ = packed.shape
-    out = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+    out = torch.empty(M, N, dtype=A.dtype, device="cuda")
     ws = torch.empty(_lib.query("xk_moe_int4_w4a16_workspace_bytes", M, ids.shape[1], E, N, K),
                      dtype=torch.uint8, device="cuda")
     _lib.call("xk_moe_int4_w4a16", *_args(A, packed, scale, ids, w, flags), out.data_ptr(),
@@ -40,7 +41,7 @@ def _with_workspace(A, packed, scale, ids, w, flags=0):
 
 
 def _no_alloc(A, packed, scale, ids, w, flags=0):
-    out = torch.empty(A.shape[0], packed.shape[1], dtype=torch.bfloat16, device="cuda")
+    out = torch.empty(A.shape[0], packed.shape[1], dtype=A.dtype, device="cuda")
     _lib.call("xk_moe_int4_w4a16_noalloc", *_args(A, packed, scale, ids, w, flags), out.data_ptr(),
               torch.cuda.current_stream().cuda_stream)
     return out
@@ -61,6 +62,22 @@ def test_no_alloc_matches_workspace_entry():
         want = _with_workspace(*x, flags=flags)
         torch.cuda.synchronize()
         assert torch.equal(got, want), f"M={M}: noalloc result differs from the workspace entry point"
+
+
+def test_no_alloc_matches_workspace_entry_fp32_activations():
+    """The same with fp32 activations (the stream kernel's split-bf16 variant,
+    four K slices at K = 7168)."""
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    for M, E, N, K, k, routing in [(64, 48, 4096, 7168, 8, "uniform"), (7, 8, 1024, 2048, 2, "zipf")]:
+        print(f"noalloc fp32 M={M} E={E} N={N} K={K} k={k}", flush=True)
+        A, packed, scale, ids, w = _inputs(M, E, N, K, k, seed=M + 50, routing=routing)
+        A = A.float()
+        got = _no_alloc(A, packed, scale, ids, w)
+        want = _with_workspace(A, packed, scale, ids, w)
+        torch.cuda.synchronize()
+        assert got.dtype == torch.float32
+        assert torch.equal(got, want), f"M={M}: noalloc fp32 result differs from the workspace entry point"
 
 
 def test_no_alloc_rejects_oversized_call():
