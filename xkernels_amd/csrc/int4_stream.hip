@@ -333,16 +333,31 @@ __device__ __forceinline__ void stream_body(const RsArgs& p) {
     if constexpr (F32A) {
       lds_sync();  // the row table is complete
       const float* A32 = reinterpret_cast<const float*>(p.A);
-      for (int t = tid; t < nblk * 64; t += kRsThreads) {
-        const int blk = t >> 6, ln = t & 63, qq = ln >> 4;
-        const int j = blk & 3, h = (blk >> 2) & 1, line = blk >> 3;
-        const int k0 = s * Ks + line * 256 + (4 * h + qq) * 32 + 8 * j;
-        const int slot = row_slot[ln & 15];
-        u32x4 vh = u32x4{0u, 0u, 0u, 0u}, vl = vh;
-        if (slot >= 0 && k0 < K) {
-          const float* a = A32 + static_cast<int64_t>(slot / p.a_row_div) * K + k0;
-          const f32x4 x0 = *reinterpret_cast<const f32x4*>(a), x1 = *reinterpret_cast<const f32x4*>(a + 4);
-          const float x[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+      // four blocks per thread in flight: their loads issue before any use
+      const int total = nblk * 64;
+      for (int t0 = tid; t0 < total; t0 += 4 * kRsThreads) {
+        f32x4 xs[4][2];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int t = t0 + u * kRsThreads;
+          const int blk = t >> 6, ln = t & 63, qq = ln >> 4;
+          const int j = blk & 3, h = (blk >> 2) & 1, line = blk >> 3;
+          const int k0 = s * Ks + line * 256 + (4 * h + qq) * 32 + 8 * j;
+          const int slot = t < total ? row_slot[ln & 15] : -1;
+          xs[u][0] = xs[u][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+          if (slot >= 0 && k0 < K) {
+            const float* a = A32 + static_cast<int64_t>(slot / p.a_row_div) * K + k0;
+            xs[u][0] = *reinterpret_cast<const f32x4*>(a);
+            xs[u][1] = *reinterpret_cast<const f32x4*>(a + 4);
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int t = t0 + u * kRsThreads;
+          if (t >= total) break;
+          const float x[8] = {xs[u][0][0], xs[u][0][1], xs[u][0][2], xs[u][0][3],
+                              xs[u][1][0], xs[u][1][1], xs[u][1][2], xs[u][1][3]};
+          u32x4 vh, vl;
 #pragma unroll
           for (int e2 = 0; e2 < 4; ++e2) {
             typedef float f2 __attribute__((ext_vector_type(2)));
@@ -353,9 +368,9 @@ __device__ __forceinline__ void stream_body(const RsArgs& p) {
             vh[e2] = hh;
             vl[e2] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f2{r0, r1}), b2));
           }
+          a_lds[t] = vh;
+          a_lds[total + t] = vl;
         }
-        a_lds[t] = vh;
-        a_lds[nblk * 64 + t] = vl;
       }
       lds_sync();
       return;
