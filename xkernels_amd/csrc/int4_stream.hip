@@ -788,7 +788,11 @@ int stream_slices(int64_t K, int64_t N, int64_t numel, int64_t E, int per_wave, 
 }
 
 #ifndef XK_MX_ITEMS_PER_WAVE
-#define XK_MX_ITEMS_PER_WAVE 8
+// MXFP4: the LDS rule only as well. At 8 pairs per wave the small batches got
+// up to 16 slices and ran slower (E = 256, hidden 4096, ispp 512, top_k 6, per
+// fused call: M = 2 43.6 -> 39.4 us, M = 8 76 -> 56 us, M = 16 96.9 -> 76.6 us,
+// M = 32 119.0 -> 115.9 us; M = 48 unchanged at 2 slices).
+#define XK_MX_ITEMS_PER_WAVE 0
 #endif
 #ifndef XK_RS_ITEMS_PER_WAVE
 // INT4: the LDS rule only. More slices for balance measured slower at the
