@@ -54,8 +54,12 @@ extern "C" {
 #define XK_DT_NONE (-1) /* "no tensor" for optional weights */
 
 /* int4 `flags` arguments: pass 0. Every dequantised weight is rounded to bf16
- * before the contraction, as the reference does; other values are rejected
- * (XK_ERR_INVALID). */
+ * before the contraction, as the reference does. Bits 8 and 9 are test-only
+ * kernel choices used by this library's GPU tests (force the prefill tile
+ * kernel / the decode stream kernel where the shapes allow both); a fused call
+ * given them returns XK_ERR_INVALID when the partial planes the forced kernel
+ * writes do not fit the workspace sized by xk_moe_int4_w4a16_workspace_bytes.
+ * Every other bit is rejected (XK_ERR_INVALID). */
 
 /* Message of the last failed call on this thread ("" if none). */
 const char* xk_last_error(void);
@@ -109,6 +113,16 @@ int xk_moe_sum_reduce(const void* y, int32_t y_dtype, int64_t M, int64_t top_k,
  * ------------------------------------------------------------------------- */
 int64_t xk_moe_int4_w4a16_workspace_bytes(int64_t M, int64_t top_k, int64_t E,
                                           int64_t N, int64_t K);
+/* The workspace for calls with an expert map over num_global_experts experts
+ * (>= the above). With an expert map the kernel choice counts the slots
+ * expected on the E local experts (M*top_k*E/num_global_experts, the rows per
+ * expert of the dense call) when the workspace holds that choice's partial
+ * planes, as one of this size does; otherwise every slot counts. The result is
+ * the same contraction either way (fp32 summation order aside). No
+ * counterpart in the reference (it has no workspace query). */
+int64_t xk_moe_int4_w4a16_ep_workspace_bytes(int64_t M, int64_t top_k, int64_t E,
+                                             int64_t N, int64_t K,
+                                             int32_t num_global_experts);
 int xk_moe_int4_w4a16(const void* A, int32_t a_dtype, int64_t M, int64_t K,
                       const int32_t* packed, const uint16_t* scale, int64_t E,
                       int64_t N, int32_t group_size, const int32_t* topk_ids,
@@ -182,7 +196,8 @@ int xk_moe_topk_combine(const float* slot_out, int64_t M, int64_t top_k,
  * experts; the k largest in descending probability, ties broken by ascending
  * expert id; with renormalize the selected weights are divided by their sum.
  * gating [M, E] bf16 | fp32 | fp16 contiguous; topk_weights fp32 [M, k],
- * topk_ids int32 [M, k]. 1 <= k <= E <= 2048.
+ * topk_ids int32 [M, k]. 1 <= k <= E (rows of more than 2048 experts take a
+ * streaming kernel: k passes over the row).
  * ------------------------------------------------------------------------- */
 int xk_moe_topk_softmax(const void* gating_output, int32_t dtype, int64_t M, int64_t E,
                         int64_t topk, int32_t renormalize, float* topk_weights,

@@ -134,6 +134,43 @@ def test_int4_rejects_bad_arguments():
     assert "workspace" in _lib.last_error()
     assert _int4(ws=None) == _lib.XK_ERR_WORKSPACE
     assert _int4(M=0, A=None, out=None) == _lib.XK_OK  # empty batch: nothing to launch
+    # flags: 0, or the test bits 8 / 9 (kernel choice); any other bit is rejected
+    # before a launch, as is a test bit whose forced kernel needs more partial
+    # planes than the workspace holds (covered on the GPU)
+    assert _int4(flags=1) == _lib.XK_ERR_INVALID
+    assert "flags" in _lib.last_error()
+    assert _int4(flags=1 << 12) == _lib.XK_ERR_INVALID
+    assert _int4(flags=1, M=0, A=None, out=None) == _lib.XK_ERR_INVALID
+    # C5 shapes: the default choice (the tile kernel) writes one partial plane and
+    # a workspace of the queried size holds one; forcing the stream kernel would
+    # write two
+    force_stream = _lib._XK_INT4_TEST_FORCE_STREAM
+    nb = _lib.query("xk_moe_int4_w4a16_workspace_bytes", 4096, 8, 48, 4096, 7168)
+    assert _int4(M=4096, K=7168, N=4096, E=48, k=8, flags=force_stream, wsb=nb) == _lib.XK_ERR_INVALID
+    assert "partial planes" in _lib.last_error()
+
+
+def test_int4_ep_workspace_covers_the_expert_parallel_choice():
+    """Under an expert map the kernel choice counts the slots expected on the
+    local experts: E = 48 local of 384 with 4096 slots is 10.7 rows per local
+    expert (the decode stream kernel, 2 K-slice planes at K = 7168), where
+    counting all slots would give 85 (the tile kernel, one plane). The expert
+    workspace query sizes for the former; without a map it equals the dense one."""
+    q = lambda *a: _lib.query("xk_moe_int4_w4a16_ep_workspace_bytes", *a)
+    dense = lambda *a: _lib.query("xk_moe_int4_w4a16_workspace_bytes", *a)
+    assert q(512, 8, 48, 4096, 7168, 0) == dense(512, 8, 48, 4096, 7168)
+    assert q(512, 8, 48, 4096, 7168, 48) == dense(512, 8, 48, 4096, 7168)
+    # C5 shapes (32768 slots): without a map fp32 activations take the scalar
+    # kernel and bf16 the tile kernel (one plane each); 48 local experts of 2048
+    # expect 16 rows each, where the bf16 choice is the stream kernel (two planes)
+    plane = 32768 * 4096 * 4
+    assert q(4096, 8, 48, 4096, 7168, 2048) - dense(4096, 8, 48, 4096, 7168) == plane
+    assert q(4096, 8, 48, 4096, 7168, 96) == dense(4096, 8, 48, 4096, 7168)  # 341 rows: tile
+
+
+def test_int4_noalloc_rejects_unknown_flags():
+    assert _rc("xk_moe_int4_w4a16_noalloc", FAKE, 0, 4, 64, FAKE, FAKE, 2, 16, 32, FAKE, FAKE, 2,
+               None, 0, 1, 4, FAKE, None) == _lib.XK_ERR_INVALID
 
 
 def test_int4_gemm_stage_rejects_bad_arguments():
@@ -191,7 +228,7 @@ def test_call_raises_with_message():
         _lib.call("xk_moe_sum_reduce", FAKE, 7, 4, 2, 8, None, 0, 1.0, FAKE, None)
 
 
-@pytest.mark.parametrize("kw", [dict(dt=3), dict(E=0), dict(E=2049, k=8), dict(k=0), dict(k=65),
+@pytest.mark.parametrize("kw", [dict(dt=3), dict(E=0), dict(E=(1 << 30) + 1, k=8), dict(k=0), dict(k=65),
                                 dict(w=None), dict(ids=None), dict(g=None), dict(M=-1)])
 def test_topk_softmax_rejects_bad_arguments(kw):
     a = dict(g=FAKE, dt=0, M=4, E=64, k=8, renorm=1, w=FAKE, ids=FAKE, stream=None)

@@ -89,6 +89,46 @@ def test_expert_parallel_partials_sum_to_dense(ep_size, dev):
     assert_close(total, dense, 3e-2, 3e-2, "EP sum")
 
 
+def _fused_capi(A, packed, scale, ids, w, emap, flags):
+    from xkernels_amd import _lib
+
+    M, K = A.shape
+    E, N, _ = packed.shape
+    k = ids.shape[1]
+    out = torch.empty(M, N, dtype=torch.bfloat16, device=A.device)
+    nb = _lib.query("xk_moe_int4_w4a16_ep_workspace_bytes", M, k, E, N, K, emap.numel())
+    ws = torch.empty(nb, dtype=torch.uint8, device=A.device)
+    _lib.call("xk_moe_int4_w4a16", A.data_ptr(), _lib.XK_DT_BF16, M, K, packed.data_ptr(),
+              scale.data_ptr(), E, N, 32, ids.data_ptr(), w.data_ptr(), k, emap.data_ptr(),
+              emap.numel(), 1, flags, out.data_ptr(), ws.data_ptr(), ws.numel(),
+              torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    return out
+
+
+def test_expert_parallel_kernel_choice_follows_local_rows(dev):
+    """16 local experts of 256 with 2048 routed slots: 8 rows per local expert,
+    so the rank runs the decode stream kernel, as the dense call over 256
+    experts does (8 rows each); counting every slot against the 16 local
+    experts (128 rows each) would have picked the prefill tile kernel. The
+    default call equals the call forced onto the stream kernel bit for bit and
+    meets the oracle."""
+    from xkernels_amd import _lib
+
+    Eg, El, M, k, N, K = 256, 16, 256, 8, 512, 1024
+    A, packed, scale, ids, w = _case(M, Eg, N, K, k, seed=31)
+    A, ids, w = A.to(dev), ids.to(dev), w.float().to(dev)
+    emap = torch.full((Eg,), -1, dtype=torch.int32, device=dev)
+    emap[64:64 + El] = torch.arange(El, dtype=torch.int32, device=dev)
+    lp = packed[64:64 + El].contiguous().to(dev)
+    ls = scale[64:64 + El].contiguous().to(dev)
+    got = _fused_capi(A, lp, ls, ids, w, emap, 0)
+    stream = _fused_capi(A, lp, ls, ids, w, emap, _lib._XK_INT4_TEST_FORCE_STREAM)
+    assert torch.equal(got, stream)
+    ref = moe_w4a16_ref(A.cpu(), lp.cpu(), ls.cpu(), ids.cpu(), w.cpu(), expert_map=emap.cpu())
+    assert_close(got, ref, 2e-2, 2e-2, "EP rank")
+
+
 def test_workspace_reuse(dev):
     ws = MoeInt4Workspace.allocate(32, 4, 256, dtype=torch.bfloat16, device=dev, num_experts=8, K=512)
     for M in (32, 7):

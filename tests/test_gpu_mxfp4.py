@@ -148,7 +148,7 @@ def test_workspace(ispp, dev):
         assert_close(got, _ref(A, wts, ids, w), 2e-2, 2e-2, f"ws M={M}")
 
 
-def _c4(scale_lo, scale_hi, a_scale=1.0):
+def _c4(scale_lo, scale_hi, a_scale=1.0, with_f64=False):
     wts = make_mxfp4_moe_weights(256, 4096, 512, device="cuda", seed=40, scale_lo=scale_lo,
                                  scale_hi=scale_hi)
     g = torch.Generator(device="cuda").manual_seed(41)
@@ -157,7 +157,10 @@ def _c4(scale_lo, scale_hi, a_scale=1.0):
     w = softmax_weights(48, 6, 43).cuda()
     got = fused_moe_mxfp4(A, *(wts[k] for k in KEYS), ids, w, backend=Backend.HIP)
     want = moe_mxfp4_ref(A, *(wts[k] for k in KEYS), ids, w)  # oracle on the device copy
-    return got.float(), want.float()
+    if not with_f64:
+        return got.float(), want.float()
+    from tests._orderings import moe_mxfp4_f64
+    return got.float(), want.float(), moe_mxfp4_f64(A, *(wts[k] for k in KEYS), ids, w).float()
 
 
 def test_config4_full_size_reference_test_scale(dev):
@@ -175,12 +178,19 @@ def test_config4_full_size(dev):
     one bf16 ulp of those intermediates (the reference rounds both) is 0.25-4.
     Two correct implementations that accumulate in different orders then differ
     by such ulps wherever the final sum cancels; the check therefore bounds the
-    relative L2 error and each element against the output's own scale."""
-    got, want = _c4(119, 128)
-    rel_l2 = float((got - want).norm() / want.norm())
-    assert rel_l2 < 2e-3, rel_l2
-    scale = float(want.abs().mean())
-    assert_close(got, want, 2e-2, 2e-2 * scale, "C4 vs output scale")
+    relative L2 error and each element against the spread that summation order
+    alone produces on these inputs: the oracle against the same pipeline with
+    float64 contractions (tests/_orderings.py; on the CPU copy of this config
+    that spread is rel-L2 8.9e-5 with 12 elements beyond the spec's 2e-2, see
+    tests/test_oracle.py). The kernel is held to 4x that spread: a kernel error
+    of 10x the ordering noise fails."""
+    from tests._orderings import rel_l2
+    got, want, alt = _c4(119, 128, with_f64=True)
+    spread = rel_l2(want, alt)
+    assert 1e-5 < spread < 1e-3, spread
+    assert rel_l2(got, want) <= 4 * spread, (rel_l2(got, want), spread)
+    worst = float((want - alt).abs().max())
+    assert float((got - want).abs().max()) <= 4 * worst, (float((got - want).abs().max()), worst)
 
 
 def test_known_answer_clamp_and_bias(dev):

@@ -29,7 +29,7 @@ def _check(g, k, renorm):
     assert not bad.any(), f"ids differ in {int(bad.sum())} rows; first {int(bad.nonzero()[0])}: " \
                           f"{ids[bad][0].tolist()} vs {rids[bad][0].tolist()}"
     rtol, atol = TOL[g.dtype]
-    torch.testing.assert_close(w, rw, rtol=rtol, atol=atol)
+    torch.testing.assert_close(w, rw, rtol=rtol, atol=atol, equal_nan=True)
 
 
 @pytest.mark.parametrize("M,E,k", [(8, 16, 4), (64, 256, 8), (37, 8, 2), (1, 256, 8), (8, 4, 1)])
@@ -41,7 +41,8 @@ def test_matches_oracle(M, E, k, dt, renorm, dev):
 
 
 @pytest.mark.parametrize("M,E,k", [(33, 65, 7), (5, 2048, 64), (3, 2048, 100), (4, 130, 130),
-                                   (9, 1, 1), (17, 384, 12), (2, 1000, 999)])
+                                   (9, 1, 1), (17, 384, 12), (2, 1000, 999),
+                                   (6, 2049, 8), (3, 5000, 70), (2, 3000, 300)])  # E > 2048: streaming kernel
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float32])
 def test_edge_shapes(M, E, k, dt, dev):
     print(f"topk_softmax M={M} E={E} k={k} {dt}", flush=True)
@@ -87,3 +88,50 @@ def test_rejects_bad_topk_and_cpu(dev):
 def test_empty_batch(dev):
     w, ids = topk_softmax(torch.empty(0, 64, device=dev), 4, backend=Backend.HIP)
     assert w.shape == ids.shape == (0, 4)
+
+
+@pytest.mark.parametrize("dt", DTYPES)
+def test_non_finite_rows(dev, dt):
+    """Rows with a NaN or +inf logit, or only -inf logits, softmax to all NaN in
+    the reference and select experts 0 .. k-1 (NaN keys rank first, ties to the
+    lower id); rows with some -inf logits select normally. Every id stays in
+    [0, E)."""
+    nan, inf = float("nan"), float("inf")
+    E = 130
+    g = torch.randn(8, E, generator=torch.Generator(device=dev).manual_seed(5), device=dev)
+    g[0, 77] = nan
+    g[1, 129] = inf
+    g[2] = -inf
+    g[3, ::2] = -inf
+    g[4, :] = -inf
+    g[4, 100] = 0.0
+    g[5, 64] = nan
+    g[5, 3] = inf
+    g = g.to(dt)
+    for k in (1, 5, 70):
+        # against the oracle on the CPU: torch's device softmax does not turn
+        # a row holding both a NaN and a +inf (row 5) into all NaN
+        for renorm in (True, False):
+            w, ids = topk_softmax(g, k, renormalize=renorm, backend=Backend.HIP)
+            rw, rids = topk_softmax_ref(g.cpu(), k, renorm)
+            assert torch.equal(ids.cpu(), rids)
+            rtol, atol = TOL[dt]
+            torch.testing.assert_close(w.cpu(), rw, rtol=rtol, atol=atol, equal_nan=True)
+        w, ids = topk_softmax(g, k, renormalize=True, backend=Backend.HIP)
+        assert int(ids.min()) >= 0 and int(ids.max()) < E
+        for r in (0, 1, 2, 5):
+            assert ids[r].tolist() == list(range(k))
+            assert torch.isnan(w[r]).all()
+        assert int(ids[4, 0]) == 100
+
+
+def test_auto_dispatch_above_2048_experts(dev):
+    """backend='auto' picks the HIP kernel for any E (rows beyond 2048 experts
+    stream), including the non-finite row semantics."""
+    g = torch.randn(5, 4100, generator=torch.Generator(device=dev).manual_seed(8), device=dev)
+    g[1, 4099] = float("nan")
+    w, ids = topk_softmax(g, 6, renormalize=True)
+    rw, rids = topk_softmax_ref(g.cpu(), 6, True)
+    assert torch.equal(ids.cpu(), rids)
+    torch.testing.assert_close(w.cpu(), rw, rtol=1e-5, atol=1e-6, equal_nan=True)
+    assert ids[1].tolist() == list(range(6))

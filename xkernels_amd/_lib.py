@@ -43,6 +43,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     ),
     "xk_moe_sum_reduce": (ctypes.c_int, [_p, _i32, _i64, _i64, _i64, _p, _i32, _f32, _p, _p]),
     "xk_moe_int4_w4a16_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64, _i64]),
+    "xk_moe_int4_w4a16_ep_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64, _i64, _i32]),
     "xk_moe_int4_w4a16": (
         ctypes.c_int,
         [_p, _i32, _i64, _i64, _p, _p, _i64, _i64, _i32, _p, _p, _i64, _p, _i32, _i32, _i32, _p,

@@ -12,6 +12,7 @@
 #include <mutex>
 
 #include "common.h"
+#include "int4_flags.h"
 
 namespace xk {
 
@@ -42,18 +43,18 @@ int launch_topk_combine(const float* slot_out, int64_t M, int64_t top_k, int64_t
                         int out_dtype, int nparts, hipStream_t stream,
                         const uint16_t* post_bias = nullptr, int post_round = 0);
 int int4_gemm_parts(int64_t M, int64_t top_k, int64_t E, int64_t N, int64_t K, int a_dtype,
-                    int group_size, int flags);
+                    int group_size, int flags, int64_t ep_global = 0);
 int int4_block_size();
 bool int4_use_stream(int a_dtype, int group_size, int64_t K);
 bool int4_gemm_self_routes(int64_t M, int64_t top_k, int64_t E, int64_t N, int64_t K, int a_dtype,
-                           int group_size, int flags);
+                           int group_size, int flags, int64_t ep_global = 0);
 int64_t int4_gemm_workspace_bytes(int64_t M, int64_t K);
 int launch_int4_gemm(const void* A, int a_dtype, int64_t M, int64_t K, const int32_t* packed,
                      const uint16_t* scale, int64_t E, int64_t N, int group_size,
                      const int32_t* topk_ids, int64_t top_k, const int32_t* emap,
                      int num_global, const int32_t* sorted_ids, const int32_t* offsets,
-                     float* slot_out, int flags, void* workspace, int64_t workspace_bytes,
-                     hipStream_t stream);
+                     float* slot_out, int flags, int64_t ep_global, void* workspace,
+                     int64_t workspace_bytes, hipStream_t stream);
 int topk_softmax_max_experts();
 int launch_topk_softmax(const void* logits, int dtype, int64_t M, int64_t E, int64_t k,
                         int renorm, float* w, int32_t* ids, hipStream_t stream);
@@ -188,14 +189,43 @@ int32_t xk_moe_int4_gemm_parts(int64_t M, int64_t top_k, int64_t E, int64_t N, i
   return int4_gemm_parts(M, top_k, E, N, K, a_dtype, group_size, flags);
 }
 
+}  // extern "C"
+
+namespace {
+// Fused INT4 scratch: the align outputs, the GEMM's own workspace, then the fp32
+// partial planes [parts, numel, N] (the rest of the workspace). The planes are
+// sized for the largest count any dtype's default kernel choice writes and,
+// under an expert map of ep_global > E experts, the expert-parallel choice's.
+int64_t int4_fused_planes(int64_t M, int64_t top_k, int64_t E, int64_t N, int64_t K,
+                          int64_t ep_global) {
+  int64_t p = std::max(int4_gemm_parts(M, top_k, E, N, K, XK_DT_BF16, 32, 0),
+                       int4_gemm_parts(M, top_k, E, N, K, XK_DT_FP32, 32, 0));
+  if (ep_global > E)
+    p = std::max<int64_t>(p, std::max(int4_gemm_parts(M, top_k, E, N, K, XK_DT_BF16, 32, 0, ep_global),
+                                      int4_gemm_parts(M, top_k, E, N, K, XK_DT_FP32, 32, 0, ep_global)));
+  return p;
+}
+int64_t int4_planes_offset(int64_t M, int64_t top_k, int64_t E, int64_t K) {
+  AlignScratch al(M * top_k, int(E), int4_block_size());
+  return al.total + round_up(int4_gemm_workspace_bytes(M, K));
+}
+int64_t int4_fused_bytes(int64_t M, int64_t top_k, int64_t E, int64_t N, int64_t K,
+                         int64_t ep_global) {
+  return int4_planes_offset(M, top_k, E, K) +
+         round_up(int4_fused_planes(M, top_k, E, N, K, ep_global) * M * top_k * N * 4);
+}
+}  // namespace
+
+extern "C" {
+
 int64_t xk_moe_int4_w4a16_workspace_bytes(int64_t M, int64_t top_k, int64_t E, int64_t N,
                                           int64_t K) {
-  const int64_t numel = M * top_k;
-  AlignScratch al(numel, int(E), int4_block_size());
-  // sized for the largest number of partial planes any mode / dtype uses
-  const int64_t parts = std::max(int4_gemm_parts(M, top_k, E, N, K, XK_DT_BF16, 32, 0),
-                                 int4_gemm_parts(M, top_k, E, N, K, XK_DT_FP32, 32, 0));
-  return al.total + round_up(parts * numel * N * 4) + round_up(int4_gemm_workspace_bytes(M, K));
+  return int4_fused_bytes(M, top_k, E, N, K, 0);
+}
+
+int64_t xk_moe_int4_w4a16_ep_workspace_bytes(int64_t M, int64_t top_k, int64_t E, int64_t N,
+                                             int64_t K, int32_t num_global_experts) {
+  return int4_fused_bytes(M, top_k, E, N, K, num_global_experts);
 }
 
 int64_t xk_moe_int4_gemm_workspace_bytes(int64_t M, int64_t K) {
@@ -212,7 +242,7 @@ int xk_moe_int4_w4a16_gemm(const void* A, int32_t a_dtype, int64_t M, int64_t K,
   clear_error();
   return launch_int4_gemm(A, a_dtype, M, K, packed, scale, E, N, group_size, topk_ids, top_k,
                           expert_map, num_global_experts, sorted_token_ids, expert_offsets,
-                          slot_out, flags, workspace, workspace_bytes, stream);
+                          slot_out, flags, 0, workspace, workspace_bytes, stream);
 }
 
 int xk_moe_topk_combine(const float* slot_out, int64_t M, int64_t top_k, int64_t N,
@@ -239,6 +269,8 @@ int xk_moe_int4_w4a16(const void* A, int32_t a_dtype, int64_t M, int64_t K,
   XK_REQUIRE(out != nullptr || M == 0, "int4: null out");
   XK_REQUIRE(M == 0 || (A && packed && scale && topk_ids), "int4: null input pointer");
   XK_REQUIRE(!mul_routed_weight || topk_w || M == 0, "int4: null topk_w");
+  XK_REQUIRE((flags & ~(XK_INT4_TEST_FORCE_TILE | XK_INT4_TEST_FORCE_STREAM)) == 0,
+             "int4: unknown flags 0x%x (pass 0)", flags);
   if (M == 0) return XK_OK;
   const int64_t need = xk_moe_int4_w4a16_workspace_bytes(M, top_k, E, N, K);
   if (workspace == nullptr || workspace_bytes < need)
@@ -246,16 +278,28 @@ int xk_moe_int4_w4a16(const void* A, int32_t a_dtype, int64_t M, int64_t K,
                      (long long)workspace_bytes, (long long)need);
   const int64_t numel = M * top_k;
   AlignScratch al(numel, int(E), int4_block_size());
-  float* slot_out = at<float>(workspace, al.total);
-  const int64_t parts = int4_gemm_parts(M, top_k, E, N, K, a_dtype, group_size, flags);
-  const int64_t gemm_ws = al.total + round_up(std::max(int4_gemm_parts(M, top_k, E, N, K, XK_DT_BF16, 32, 0),
-                                                       int4_gemm_parts(M, top_k, E, N, K, XK_DT_FP32, 32, 0)) *
-                                              numel * N * 4);
+  const int64_t planes_at = int4_planes_offset(M, top_k, E, K);
+  float* slot_out = at<float>(workspace, planes_at);
+  const int64_t planes_held = (workspace_bytes - planes_at) / (numel * N * 4);
+  // Under an expert map the kernel choice counts the slots expected on the
+  // local experts (the dense call's rows per expert) when the workspace holds
+  // the partial planes of that choice (xk_moe_int4_w4a16_ep_workspace_bytes
+  // sizes for it); else, and with the test bits, every slot counts.
+  int64_t ep_global = 0;
+  if (flags == 0 && expert_map != nullptr && num_global_experts > E &&
+      int4_gemm_parts(M, top_k, E, N, K, a_dtype, group_size, 0, num_global_experts) <= planes_held)
+    ep_global = num_global_experts;
+  const int64_t parts = int4_gemm_parts(M, top_k, E, N, K, a_dtype, group_size, flags, ep_global);
+  // the test bits may force a kernel that writes more partial planes than the
+  // default choices the workspace is sized for
+  XK_REQUIRE(parts <= planes_held,
+             "int4: flags=0x%x need %lld partial planes, more than the workspace holds", flags,
+             (long long)parts);
   const int32_t* sorted = nullptr;
   const int32_t* offsets = nullptr;
   // the decode kernel routes for itself; the other MFMA kernels take the align
   if (int4_use_stream(a_dtype, group_size, K) &&
-      !int4_gemm_self_routes(M, top_k, E, N, K, a_dtype, group_size, flags)) {
+      !int4_gemm_self_routes(M, top_k, E, N, K, a_dtype, group_size, flags, ep_global)) {
     int rc = launch_align(topk_ids, numel, int(E), int4_block_size(), expert_map,
                           num_global_experts, at<int32_t>(workspace, al.sorted),
                           at<int32_t>(workspace, al.expert_ids),
@@ -268,7 +312,7 @@ int xk_moe_int4_w4a16(const void* A, int32_t a_dtype, int64_t M, int64_t K,
   }
   if (int rc = launch_int4_gemm(A, a_dtype, M, K, packed, scale, E, N, group_size, topk_ids,
                                 top_k, expert_map, num_global_experts, sorted, offsets,
-                                slot_out, flags, at<char>(workspace, gemm_ws),
+                                slot_out, flags, ep_global, at<char>(workspace, al.total),
                                 round_up(int4_gemm_workspace_bytes(M, K)), stream))
     return rc;
   return launch_topk_combine(slot_out, M, top_k, N, topk_w, mul_routed_weight, topk_ids,
@@ -289,6 +333,8 @@ int xk_moe_int4_w4a16_noalloc(const void* A, int32_t a_dtype, int64_t M, int64_t
   XK_REQUIRE(M >= 0 && top_k >= 1 && E >= 1 && N >= 1 && K >= 1,
              "int4 noalloc: bad sizes M=%lld top_k=%lld E=%lld N=%lld K=%lld", (long long)M,
              (long long)top_k, (long long)E, (long long)N, (long long)K);
+  XK_REQUIRE((flags & ~(XK_INT4_TEST_FORCE_TILE | XK_INT4_TEST_FORCE_STREAM)) == 0,
+             "int4 noalloc: unknown flags 0x%x (pass 0)", flags);
   if (M == 0) return XK_OK;
   const int64_t need = xk_moe_int4_w4a16_workspace_bytes(M, top_k, E, N, K);
   XK_REQUIRE(need <= xk::kNoAllocScratchBytes,
@@ -328,15 +374,11 @@ namespace {
 // activations, shapes within its limits), else the per-stage kernels.
 // Workspace after the align scratch: act [numel, ispp] bf16, then the down
 // projection's rows [S1, numel, hidden] fp32, then (stream path) the gate/up
-// planes [S0, numel, 2 ispp] fp32. The slice counts grow as batches shrink,
-// so each plane region is sized for the largest S(n) n over n <= numel: the
-// workspace bytes never decrease with M, and a workspace sized for a batch
+// planes [S0, numel, 2 ispp] fp32. The slice counts depend on K only, so the
+// workspace bytes never decrease with M and a workspace sized for a batch
 // serves every smaller one.
 int64_t max_plane_rows(int64_t K, int64_t N, int64_t numel, int64_t E) {
-  int64_t best = mxfp4_rs_slices(K, N, numel, E) * numel;
-  for (int64_t n = 1; n < std::min(numel, E); ++n)  // S(n) is constant from n = E on
-    best = std::max<int64_t>(best, mxfp4_rs_slices(K, N, n, E) * n);
-  return best;
+  return mxfp4_rs_slices(K, N, numel, E) * numel;
 }
 
 constexpr int64_t kMxStreamRowsPerExpert = 20;

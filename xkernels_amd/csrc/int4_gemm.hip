@@ -115,14 +115,20 @@ int64_t int4_gemm_workspace_bytes(int64_t M, int64_t K) {
 // call. Pointer alignment the chosen kernel needs is checked at launch.
 enum class Int4Kernel { kSimple, kRs, kTile };
 
+// ep_global > E: the call runs E local experts of ep_global under an expert
+// map; the routed rows per local expert are then estimated as those of the
+// dense call (numel * E / ep_global slots expected on the local experts), so
+// that an expert-parallel rank picks the kernel the dense call picks for the
+// same rows per expert. 0: every slot counts against the E experts.
 Int4Kernel int4_choose(int64_t M, int64_t top_k, int64_t E, int64_t N, int64_t K, int a_dtype,
-                       int group_size, int flags) {
+                       int group_size, int flags, int64_t ep_global) {
   if (!int4_use_stream(a_dtype, group_size, K)) return Int4Kernel::kSimple;
   const int64_t numel = M * top_k;
+  const int64_t local = ep_global > E ? (numel * E + ep_global - 1) / ep_global : numel;
   const bool f32a = a_dtype == XK_DT_FP32;
   const bool tile_ok = !f32a && int4_prefill_ok(a_dtype, group_size, K, N, E);
   const bool rs_ok = int4_rs_ok(M, top_k, K, N, E, f32a);
-  bool tile = tile_ok && numel >= kPrefillRowsPerExpert * E;
+  bool tile = tile_ok && local >= kPrefillRowsPerExpert * E;
   if (flags & XK_INT4_TEST_FORCE_TILE) tile = tile_ok;
   if (flags & XK_INT4_TEST_FORCE_STREAM) tile = tile && !rs_ok;
   if (tile) return Int4Kernel::kTile;
@@ -133,8 +139,8 @@ Int4Kernel int4_choose(int64_t M, int64_t top_k, int64_t E, int64_t N, int64_t K
 // Number of fp32 partial planes [parts, M * top_k, N] the grouped GEMM
 // writes: the K slices of the decode stream kernel, else one.
 int int4_gemm_parts(int64_t M, int64_t top_k, int64_t E, int64_t N, int64_t K, int a_dtype,
-                    int group_size, int flags) {
-  return int4_choose(M, top_k, E, N, K, a_dtype, group_size, flags) == Int4Kernel::kRs
+                    int group_size, int flags, int64_t ep_global) {
+  return int4_choose(M, top_k, E, N, K, a_dtype, group_size, flags, ep_global) == Int4Kernel::kRs
              ? int4_rs_slices(K, N, M * top_k, E, a_dtype == XK_DT_FP32)
              : 1;
 }
@@ -142,8 +148,8 @@ int int4_gemm_parts(int64_t M, int64_t top_k, int64_t E, int64_t N, int64_t K, i
 // True when launch_int4_gemm may be called without align outputs (the decode
 // kernel then routes the slots itself).
 bool int4_gemm_self_routes(int64_t M, int64_t top_k, int64_t E, int64_t N, int64_t K, int a_dtype,
-                           int group_size, int flags) {
-  return int4_choose(M, top_k, E, N, K, a_dtype, group_size, flags) == Int4Kernel::kRs &&
+                           int group_size, int flags, int64_t ep_global) {
+  return int4_choose(M, top_k, E, N, K, a_dtype, group_size, flags, ep_global) == Int4Kernel::kRs &&
          int4_rs_self_route_ok(M * top_k);
 }
 
@@ -151,8 +157,8 @@ int launch_int4_gemm(const void* A, int a_dtype, int64_t M, int64_t K, const int
                      const uint16_t* scale, int64_t E, int64_t N, int group_size,
                      const int32_t* topk_ids, int64_t top_k, const int32_t* emap,
                      int num_global, const int32_t* sorted_ids, const int32_t* offsets,
-                     float* slot_out, int flags, void* workspace, int64_t workspace_bytes,
-                     hipStream_t stream) {
+                     float* slot_out, int flags, int64_t ep_global, void* workspace,
+                     int64_t workspace_bytes, hipStream_t stream) {
   (void)workspace;
   (void)workspace_bytes;
   XK_REQUIRE(a_dtype == XK_DT_BF16 || a_dtype == XK_DT_FP32, "int4: bad A dtype %d", a_dtype);
@@ -166,7 +172,7 @@ int launch_int4_gemm(const void* A, int a_dtype, int64_t M, int64_t K, const int
   const int64_t numel = M * top_k;
   XK_REQUIRE(numel < (int64_t(1) << 30), "int4: M*top_k too large");
   if (numel == 0) return XK_OK;
-  const Int4Kernel kern = int4_choose(M, top_k, E, N, K, a_dtype, group_size, flags);
+  const Int4Kernel kern = int4_choose(M, top_k, E, N, K, a_dtype, group_size, flags, ep_global);
   // the decode kernel routes for itself when no align outputs are given
   const bool self_route = kern == Int4Kernel::kRs && sorted_ids == nullptr && offsets == nullptr &&
                           int4_rs_self_route_ok(numel);

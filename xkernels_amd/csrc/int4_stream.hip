@@ -53,21 +53,8 @@
 //     weights split exactly into bf16 hi + lo, three MFMAs per fragment.
 #include "int4_common.h"
 
-#ifndef XK_RS_VARIANT
-#define XK_RS_VARIANT 0  // diagnostic builds only: 2 no MFMA, 3 loads only
-#endif
-#ifndef XK_RS_PAIRED
-#define XK_RS_PAIRED 1  // diagnostic builds: 0 splits (expert, pass, slice, pair) items unpaired
-#endif
-#ifndef XK_RS_SPLIT
-#define XK_RS_SPLIT 1
-#endif
-#ifndef XK_RS_LOAD_POLICY
-#define XK_RS_LOAD_POLICY 0  // diagnostic builds: cache policy bits of the weight / scale loads
-#endif
-#ifndef XK_RS_STORE_POLICY
-#define XK_RS_STORE_POLICY 2  // nt: the partial rows are not re-read by this kernel
-#endif
+// cache policy of the partial-row stores: nt (this kernel never re-reads them)
+constexpr int kRsStorePolicy = 2;
 
 namespace xk {
 
@@ -75,26 +62,11 @@ int device_cu_count();
 
 namespace {
 
-#ifndef XK_RS_WAVES
-#define XK_RS_WAVES 8
-#endif
-#ifndef XK_RS_RING
-#define XK_RS_RING 2
-#endif
-#ifndef XK_RS_MAXCP
-#define XK_RS_MAXCP 3
-#endif
-constexpr int kRsWaves = XK_RS_WAVES;       // waves per workgroup (one workgroup per CU)
+constexpr int kRsWaves = 8;                 // waves per workgroup (one workgroup per CU)
 constexpr int kRsThreads = kRsWaves * 64;
-constexpr int kRsMaxCp = XK_RS_MAXCP;       // column pairs per wave per chunk
-#ifndef XK_RS_KEEP
-#define XK_RS_KEEP 9
-#endif
-constexpr int kRsKeep = XK_RS_KEEP;         // finished column pairs a wave holds before writing
-#ifndef XK_RS_SCLINES
-#define XK_RS_SCLINES 8
-#endif
-constexpr int kRsScLines = XK_RS_SCLINES;   // lines per block of group scales (4 or 8)
+constexpr int kRsMaxCp = 3;                 // column pairs per wave per chunk
+constexpr int kRsKeep = 9;                  // finished column pairs a wave holds before writing
+constexpr int kRsScLines = 8;               // lines per block of group scales
 // Weight formats of the stream: the INT4 W4A16 layout (uint4 nibbles, bf16
 // group scales, zero point 8) and MXFP4 (e2m1 nibbles, e8m0 group scales).
 // Both pack 32 elements of a group into 16 bytes, low nibble first.
@@ -104,7 +76,7 @@ template <int FMT> struct RsFmt {
   static constexpr int kLinesPerLoad = 16 / (8 * kScaleBytes);  // lines per 16-byte scale load
   static constexpr int kScLoads = kRsScLines / (4 * kLinesPerLoad);  // per lane and column tile
 };
-constexpr int kRsRing = XK_RS_RING;         // ring slots: lines k+1 .. k+R-1 in flight while line k computes
+constexpr int kRsRing = 2;                    // ring slots: lines k+1 .. k+R-1 in flight while line k computes
 constexpr int kRsLdsA = 112 * 1024;         // bytes of LDS for one activation slice
 constexpr int kRsMaxE = 512;
 constexpr int kRsMaxSelf = 4096;            // routed slots a workgroup can route for itself
@@ -207,15 +179,6 @@ __device__ __forceinline__ f32x4 quad_transpose(f32x4 e) {
 // 2^-16 of the product): about 2^-15 relative error per term, against the
 // spec's fp32 tolerance of 1e-3. The two activation planes halve the K a
 // slice holds.
-#if XK_RS_TIMELINE
-// diagnostic builds: per-workgroup phase timestamps (s_memrealtime, 100 MHz)
-// of the last launch per K: [K == 4096 ? 0 : 1][block][phase]
-__device__ unsigned long long xk_tl[2][256][6];
-__device__ unsigned long long xk_tlw[2][256][16];
-#define XK_TL(ph) do { if (threadIdx.x == 0 && blockIdx.x < 256) xk_tl[p.K == 4096 ? 0 : 1][blockIdx.x][ph] = __builtin_amdgcn_s_memrealtime(); } while (0)
-#else
-#define XK_TL(ph) do { } while (0)
-#endif
 template <int FMT, bool PADK, bool F32A = false>
 __device__ __forceinline__ void stream_body(const RsArgs& p) {
   using F = RsFmt<FMT>;
@@ -229,7 +192,6 @@ __device__ __forceinline__ void stream_body(const RsArgs& p) {
   __shared__ int left_lds[kRsWaves];  // INT4: steps each wave has left
   int left = 0;
 
-  XK_TL(0);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = uniform(tid >> 6);
 
@@ -237,7 +199,7 @@ __device__ __forceinline__ void stream_body(const RsArgs& p) {
   const int K = p.K, N = p.N, E = p.E, G = K >> 5, KW = K >> 3;
   // K is cut into 256-k lines, the last one zero-padded when K % 256 != 0
   const int S = p.slices, nl = ((K + 255) >> 8) / S, Ks = nl << 8;
-  const bool paired = XK_RS_PAIRED && S > 1 && gridDim.x % (8 * S) == 0;
+  const bool paired = S > 1 && gridDim.x % (8 * S) == 0;
   const int ncp = N >> 5;            // column pairs per expert
   const int nblk = nl * 8;           // 1 KiB operand blocks of one activation slice
   const uint32_t kNibMask = in_vgpr(0x000F000Fu), kNibMaskHi = in_vgpr(0x00F000F0u);
@@ -281,7 +243,6 @@ __device__ __forceinline__ void stream_body(const RsArgs& p) {
   // scales that straddle a slice boundary (a column's scale row is K / 16
   // bytes, not a multiple of 128) are fetched once for both. Otherwise the
   // items (expert, pass, slice, column pair) are split evenly.
-  XK_TL(1);
   const int total_items = uniform(pref[E]);
   const int b = blockIdx.x;
   const int gsz = paired ? static_cast<int>(gridDim.x) / S : static_cast<int>(gridDim.x);
@@ -297,11 +258,49 @@ __device__ __forceinline__ void stream_body(const RsArgs& p) {
   const i32x4 ra = make_rsrc(p.A, p.a_bytes);
   const int64_t plane = static_cast<int64_t>(p.numel) * N;
 
+  // INT4: the two waves of a SIMD (w and w ^ 4) finish together when the
+  // one with more steps left gets the issue priority; without it the older
+  // wave wins the arbitration and the younger one runs its last pairs alone
+  // (C2 per-wave end times 114 vs 144 us; GEMM 166.5 -> 161.8 us). Each wave
+  // first counts the steps of its share (the same walk as the main one, no
+  // loads), while the first segment's loads are in flight.
+  auto count_steps = [&]() __attribute__((always_inline)) {
+  if constexpr (FMT == kFmtInt4) {
+    int rot2 = 0, pos2 = item_beg;
+    while (pos2 < item_end) {
+      int lo = 0, hi = E;
+      while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (pref[mid] <= pos2) lo = mid; else hi = mid;
+      }
+      const int e = uniform(lo);
+      const int local = pos2 - pref[e];
+      const int cp0 = local % ncp;
+      const int cpe = min(ncp, cp0 + (item_end - pos2));
+      for (int c0 = cp0; c0 < cpe; c0 += kRsWaves * kRsMaxCp) {
+        const int lc = min(kRsWaves * kRsMaxCp, cpe - c0);
+        const int base = lc / kRsWaves, rem = lc % kRsWaves;
+        const int r = (wave - rot2 + kRsWaves) % kRsWaves;
+        const int cnt = base + (r < rem ? 1 : 0);
+        if (cnt > 0) left += (cnt * nl + kRsRing - 1) / kRsRing * kRsRing;
+        rot2 = (rot2 + rem) % kRsWaves;
+      }
+      pos2 += cpe - cp0;
+    }
+    left_lds[wave] = left;  // read after the first segment's barrier
+  }
+  };
+
   // Activation slice of a segment -> LDS, in operand order: 1 KiB block
   // blk = (line * 2 + h) * 4 + j holds, at lane qq * 16 + r, the 8 values
   // k = s Ks + line * 256 + (4 h + qq) * 32 + 8 j .. + 7 of row r, in k
   // order. Rows of pad slots read token 0 (never stored).
-  auto load_segment = [&](int e, int pass, int s) __attribute__((always_inline)) {
+  // `first`: the workgroup's first segment; each wave counts its steps while
+  // the activation loads are in flight. (Pulling the first weight lines of
+  // each wave into L2 meanwhile, by direct-to-LDS loads into its scale area,
+  // measured slower: the headline GEMM 166 -> 168 / 169 / 170 us at 2 / 3 / 4
+  // lines per wave.)
+  auto load_segment = [&](int e, int pass, int s, bool first) __attribute__((always_inline)) {
     lds_sync();  // every wave is done with the previous segment
     int sid;
     if (self_route) {
@@ -372,6 +371,7 @@ __device__ __forceinline__ void stream_body(const RsArgs& p) {
           a_lds[total + t] = vl;
         }
       }
+      if (first) count_steps();
       lds_sync();
       return;
     }
@@ -382,6 +382,7 @@ __device__ __forceinline__ void stream_body(const RsArgs& p) {
       const int j = blk & 3, h = (blk >> 2) & 1, line = blk >> 3;
       dma_16(ra, &a_lds[blk * 64], a_voff, (s * Ks + line * 256 + 128 * h + 8 * j) * 2);
     }
+    if (first) count_steps();  // while the loads are in flight
     XK_WAIT_VMCNT(0);
     lds_sync();
     if constexpr (PADK) {
@@ -420,9 +421,9 @@ __device__ __forceinline__ void stream_body(const RsArgs& p) {
       if (decltype(I)::value < nkeep) {
         const f32x4 d0 = quad_transpose(keep[I][0]), d1 = quad_transpose(keep[I][1]);
         __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, d0), ro, keep_off[I], 0,
-                                               XK_RS_STORE_POLICY);
+                                               kRsStorePolicy);
         __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, d1), ro, keep_off[I] + 64, 0,
-                                               XK_RS_STORE_POLICY);
+                                               kRsStorePolicy);
       }
     });
     nkeep = 0;
@@ -465,7 +466,7 @@ __device__ __forceinline__ void stream_body(const RsArgs& p) {
 #pragma unroll
         for (int h = 0; h < 2; ++h)
           sl.w[c][h] = __builtin_amdgcn_raw_buffer_load_b128(rw, w_lane + 64 * h, wo + c * 16 * KW * 4,
-                                                             XK_RS_LOAD_POLICY);
+                                                             0);
         if (blk) {  // lanes past the slice's last line read nothing (offset past the buffer)
 #pragma unroll
           for (int i = 0; i < F::kScLoads; ++i)
@@ -475,10 +476,10 @@ __device__ __forceinline__ void stream_body(const RsArgs& p) {
 #pragma unroll
               for (int d = 0; d < 4; ++d)
                 sl.s[c][i][d] = __builtin_amdgcn_raw_buffer_load_b32(rs, voff + 4 * d, so + c * 16 * G * SB,
-                                                                     XK_RS_LOAD_POLICY);
+                                                                     0);
             } else {
               sl.s[c][i] = __builtin_amdgcn_raw_buffer_load_b128(rs, voff, so + c * 16 * G * SB,
-                                                                 XK_RS_LOAD_POLICY);
+                                                                 0);
             }
           }
         }
@@ -537,24 +538,13 @@ __device__ __forceinline__ void stream_body(const RsArgs& p) {
           [[maybe_unused]] bf16x8 blo[2];
 #pragma unroll
           for (int c = 0; c < 2; ++c) {
-#if XK_RS_VARIANT == 3
-            bfrag[c] = __builtin_bit_cast(bf16x8, sl.w[c][h]);
-#else
             if constexpr (F32A)
               dequant_split_nat(sl.w[c][h][j], ks[c], kNibMask, kNibMaskHi, bfrag[c], blo[c]);
             else if constexpr (FMT == kFmtInt4)
               bfrag[c] = dequant_rne_nat(sl.w[c][h][j], ks[c], kNibMask, kNibMaskHi);
             else
               bfrag[c] = fp4x8_to_bf16(fnan[c] ? 0u : sl.w[c][h][j], fs[c]);
-#endif
           }
-#if XK_RS_VARIANT == 2 || XK_RS_VARIANT == 3
-#pragma unroll
-          for (int c = 0; c < 2; ++c) {
-            const u32x4 x = __builtin_bit_cast(u32x4, bfrag[c]);
-            acc[c][j] = __uint_as_float(__float_as_uint(acc[c][j]) ^ x[0] ^ x[1] ^ x[2] ^ x[3]);
-          }
-#else
           const bf16x8 afrag = __builtin_bit_cast(bf16x8, a_lds[lbase + (h * 4 + j) * 64]);
           if constexpr (F32A) {
             const bf16x8 alo = __builtin_bit_cast(bf16x8, a_lds[nblk * 64 + lbase + (h * 4 + j) * 64]);
@@ -569,7 +559,6 @@ __device__ __forceinline__ void stream_body(const RsArgs& p) {
             for (int c = 0; c < 2; ++c)
               acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(afrag, bfrag[c], acc[c], 0, 0, 0);
           }
-#endif
         }
       }
     };
@@ -633,38 +622,6 @@ __device__ __forceinline__ void stream_body(const RsArgs& p) {
 
   // Walk this workgroup's item range: segments of one (expert, pass, slice),
   // cut into chunks of at most kRsWaves * kRsMaxCp column pairs.
-  // INT4: the two waves of a SIMD (w and w ^ 4) finish together when the
-  // one with more steps left gets the issue priority; without it the older
-  // wave wins the arbitration and the younger one runs its last pairs alone
-  // (C2 per-wave end times 114 vs 144 us; GEMM 166.5 -> 161.8 us). Each wave
-  // first counts the steps of its share (the same walk as below, no loads).
-  if constexpr (FMT == kFmtInt4) {
-    int rot2 = 0, pos2 = item_beg;
-    while (pos2 < item_end) {
-      int lo = 0, hi = E;
-      while (hi - lo > 1) {
-        const int mid = (lo + hi) >> 1;
-        if (pref[mid] <= pos2) lo = mid; else hi = mid;
-      }
-      const int e = uniform(lo);
-      const int local = pos2 - pref[e];
-      const int cp0 = local % ncp;
-      const int cpe = min(ncp, cp0 + (item_end - pos2));
-      for (int c0 = cp0; c0 < cpe; c0 += kRsWaves * kRsMaxCp) {
-        const int lc = min(kRsWaves * kRsMaxCp, cpe - c0);
-        const int base = lc / kRsWaves, rem = lc % kRsWaves;
-        const int r = (wave - rot2 + kRsWaves) % kRsWaves;
-        const int cnt = base + (r < rem ? 1 : 0);
-        if (cnt > 0) left += (cnt * nl + kRsRing - 1) / kRsRing * kRsRing;
-        rot2 = (rot2 + rem) % kRsWaves;
-      }
-      pos2 += cpe - cp0;
-    }
-    left_lds[wave] = left;  // read after the first segment's barrier
-#if XK_RS_TIMELINE
-    if (lane == 0 && blockIdx.x < 256) xk_tlw[p.K == 4096 ? 0 : 1][blockIdx.x][8 + wave] = left;
-#endif
-  }
   int loaded = -1;  // first item of the segment whose activations are in LDS
   int rot = 0;      // first wave to take a remainder pair in the next chunk
   int pos = item_beg;
@@ -681,38 +638,24 @@ __device__ __forceinline__ void stream_body(const RsArgs& p) {
     const int cpe = min(ncp, cp0 + (item_end - pos));
     const int seg_id = uniform(pos - cp0);
     if (seg_id != loaded) {
-      load_segment(e, pass, s);
-      if (loaded < 0) XK_TL(2);
+      load_segment(e, pass, s, loaded < 0);
       loaded = seg_id;
     }
     for (int c0 = cp0; c0 < cpe; c0 += kRsWaves * kRsMaxCp) {
       const int lc = min(kRsWaves * kRsMaxCp, cpe - c0);
       // lc / 8 pairs each, the remainder to consecutive waves from a rotating
       // start: wave w runs on SIMD w % 4, so the extra pairs spread over the
-      // SIMDs and across chunks (XK_RS_SPLIT 0: the plain proportional split)
-#if XK_RS_SPLIT
+      // SIMDs and across chunks
       const int base = lc / kRsWaves, rem = lc % kRsWaves;
       const int r = (wave - rot + kRsWaves) % kRsWaves;
       const int my_lo = c0 + r * base + min(r, rem);
       const int cnt = base + (r < rem ? 1 : 0);
       rot = (rot + rem) % kRsWaves;
-#else
-      const int my_lo = c0 + wave * lc / kRsWaves;
-      const int cnt = c0 + (wave + 1) * lc / kRsWaves - my_lo;
-#endif
       run_chunk(e, s, my_lo, cnt);
     }
     pos += cpe - cp0;
   }
-  XK_TL(3);
-#if XK_RS_TIMELINE
-  if (lane == 0 && blockIdx.x < 256) xk_tlw[p.K == 4096 ? 0 : 1][blockIdx.x][wave] = __builtin_amdgcn_s_memrealtime();
-#endif
   write_kept();
-#if XK_RS_TIMELINE
-  __syncthreads();
-#endif
-  XK_TL(4);
 }
 
 __global__ void __launch_bounds__(kRsThreads)
@@ -773,41 +716,21 @@ int rs_slices(int64_t K, bool f32a) {
   return 0;
 }
 
-// K slices of a stream launch: as many as the LDS needs, and more (up to
-// the slice count that still divides the lines) while the work items would
-// give a wave of the grid fewer than `per_wave` column pairs, since a
-// workgroup's waves finish together only if each holds several items. The
-// estimate takes every routed slot on its own expert (at most E).
-int stream_slices(int64_t K, int64_t N, int64_t numel, int64_t E, int per_wave, bool f32a) {
-  int s = rs_slices(K, f32a);
-  if (s == 0) return 0;
-  const int64_t lines = (K + 255) / 256, waves = int64_t(device_cu_count()) * kRsWaves;
-  const int64_t pairs = std::min(E, numel) * (N / 32);
-  while (pairs * s < per_wave * waves && lines % (2 * s) == 0) s *= 2;
-  return s;
-}
-
-#ifndef XK_MX_ITEMS_PER_WAVE
-// MXFP4: the LDS rule only as well. At 8 pairs per wave the small batches got
-// up to 16 slices and ran slower (E = 256, hidden 4096, ispp 512, top_k 6, per
-// fused call: M = 2 43.6 -> 39.4 us, M = 8 76 -> 56 us, M = 16 96.9 -> 76.6 us,
-// M = 32 119.0 -> 115.9 us; M = 48 unchanged at 2 slices).
-#define XK_MX_ITEMS_PER_WAVE 0
-#endif
-#ifndef XK_RS_ITEMS_PER_WAVE
-// INT4: the LDS rule only. More slices for balance measured slower at the
-// decode shapes (C2 at 4 slices 180 vs 172 us, the N = 7168, K = 2048 down
-// projection at 2 slices 93 vs 88 us): a slice costs its activation loads
-// and partial plane more than the balance gains.
-#define XK_RS_ITEMS_PER_WAVE 0
-#endif
-
+// K slices of a stream launch: the fewest the LDS allows. More slices for the
+// work balance of small batches measured slower (INT4: the headline shape at
+// 4 slices 180 vs 172 us, the N = 7168, K = 2048 down projection at 2 slices
+// 93 vs 88 us; MXFP4 at E = 256, hidden 4096, ispp 512, top_k 6 per fused
+// call: M = 8 56 -> 76 us, M = 16 76.6 -> 96.9 us with up to 16 slices): a
+// slice costs its activation loads and partial plane more than the balance
+// gains.
 int int4_rs_slices(int64_t K, int64_t N, int64_t numel, int64_t E, bool f32a) {
-  return stream_slices(K, N, numel, E, XK_RS_ITEMS_PER_WAVE, f32a);
+  (void)N; (void)numel; (void)E;
+  return rs_slices(K, f32a);
 }
 
 int mxfp4_rs_slices(int64_t K, int64_t N, int64_t numel, int64_t E) {
-  return stream_slices(K, N, numel, E, XK_MX_ITEMS_PER_WAVE, false);
+  (void)N; (void)numel; (void)E;
+  return rs_slices(K, false);
 }
 
 bool int4_rs_ok(int64_t M, int64_t top_k, int64_t K, int64_t N, int64_t E, bool f32a) {
@@ -865,10 +788,3 @@ int launch_mxfp4_rs(const void* A, int64_t a_rows, int64_t K, const uint8_t* w, 
 
 }  // namespace xk
 
-#if XK_RS_TIMELINE
-extern "C" int xk_debug_timeline(void* host) {
-  if (hipMemcpyFromSymbol(host, HIP_SYMBOL(xk::xk_tl), sizeof(xk::xk_tl)) != hipSuccess) return 1;
-  return hipMemcpyFromSymbol(static_cast<char*>(host) + sizeof(xk::xk_tl), HIP_SYMBOL(xk::xk_tlw),
-                             sizeof(xk::xk_tlw)) == hipSuccess ? 0 : 1;
-}
-#endif

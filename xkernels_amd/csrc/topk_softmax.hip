@@ -12,7 +12,8 @@
 // Selections are staged in LDS so the renormalisation and the [M, k] output
 // writes are contiguous across lanes.
 //
-// HBM bound: M*E logits in, M*k (weight, id) pairs out; no scratch.
+// HBM bound: M*E logits in, M*k (weight, id) pairs out; no scratch. Rows of
+// more than 2048 experts take a streaming variant (below).
 #include <stdint.h>
 
 #include "common.h"
@@ -38,8 +39,15 @@ __device__ __forceinline__ float logit_at<float>(const float* p) {
   return *p;
 }
 
-// a ranks before b: larger probability, or equal probability and lower id
+// a ranks before b in the reference's stable descending sort (torch.sort,
+// topk_softmax.py:88): NaN above every number, then larger probability; equal
+// keys (NaN and NaN included) to the lower id. A row with a NaN or +inf logit,
+// or only -inf logits, softmaxes to all NaN (as torch's does: the NaN or the
+// inf - inf reaches the sum), so it selects experts 0 .. k-1 with NaN weights.
 __device__ __forceinline__ bool ranks_before(float a, int ia, float b, int ib) {
+  const bool an = __builtin_isnan(a), bn = __builtin_isnan(b);
+  if (an != bn) return an;
+  if (an) return ia < ib;
   return a > b || (a == b && ia < ib);
 }
 
@@ -104,7 +112,9 @@ topk_softmax_rows(const T* __restrict__ logits, int64_t M, int E, int k, int ren
         }
       }
       // every lane now holds the same winner (bv, bid)
-      if (lane == (bid & 63)) taken |= 1u << (bid >> 6);
+      // (the winner is a real expert: k <= E, and every expert ranks before
+      // the padding's -1)
+      if (lane == (bid & 63) && (bid >> 6) < VPT) taken |= 1u << (bid >> 6);
       if (lane == 0) {
         sel_w[t] = bv;
         sel_id[t] = bid;
@@ -122,6 +132,63 @@ topk_softmax_rows(const T* __restrict__ logits, int64_t M, int E, int k, int ren
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+}
+
+// Rows of more than 32 * 64 experts: the same selection without holding the
+// row in registers. Round t re-reads the row (from L2) and takes the best
+// expert that ranks after round t-1's winner (the ranking is a total order,
+// so no taken-set is needed): k * E reads and exponentials per row. The lane
+// t % 64 writes the t-th selection; the renormalisation then rescales each
+// lane's own writes.
+template <typename T>
+__global__ void __launch_bounds__(kTsThreads)
+topk_softmax_rows_stream(const T* __restrict__ logits, int64_t M, int E, int k, int renorm,
+                         float* __restrict__ w_out, int32_t* __restrict__ id_out) {
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  for (int64_t row = int64_t(blockIdx.x) * kTsWaves + wave; row < M;
+       row += int64_t(gridDim.x) * kTsWaves) {
+    const T* g = logits + row * E;
+    float mx = -__builtin_inff();
+    for (int e = lane; e < E; e += 64) mx = fmaxf(mx, logit_at<T>(g + e));
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+    float sum = 0.f;
+    for (int e = lane; e < E; e += 64) sum += expf(logit_at<T>(g + e) - mx);
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) sum += __shfl_xor(sum, off);
+    float pv = 0.f, picked_sum = 0.f;
+    int pid = -1;  // no previous winner
+    for (int t = 0; t < k; ++t) {
+      float bv = -2.f;
+      int bid = 0x7fffffff;
+      for (int e = lane; e < E; e += 64) {
+        const float v = expf(logit_at<T>(g + e) - mx) / sum;
+        if ((pid < 0 || ranks_before(pv, pid, v, e)) && ranks_before(v, e, bv, bid)) {
+          bv = v;
+          bid = e;
+        }
+      }
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) {
+        const float ov = __shfl_xor(bv, off);
+        const int oid = __shfl_xor(bid, off);
+        if (ranks_before(ov, oid, bv, bid)) {
+          bv = ov;
+          bid = oid;
+        }
+      }
+      if (lane == (t & 63)) {
+        w_out[row * k + t] = bv;
+        id_out[row * k + t] = bid;
+      }
+      picked_sum += bv;
+      pv = bv;
+      pid = bid;
+    }
+    if (renorm)
+      for (int t = lane; t < k; t += 64) w_out[row * k + t] = w_out[row * k + t] / picked_sum;
   }
 }
 
@@ -145,12 +212,19 @@ hipError_t launch_typed(const void* logits, int64_t M, int E, int k, int renorm,
   if (per_lane <= 4) return launch_vpt<T, 4>(logits, M, E, k, renorm, w, ids, stream);
   if (per_lane <= 8) return launch_vpt<T, 8>(logits, M, E, k, renorm, w, ids, stream);
   if (per_lane <= 16) return launch_vpt<T, 16>(logits, M, E, k, renorm, w, ids, stream);
-  return launch_vpt<T, 32>(logits, M, E, k, renorm, w, ids, stream);
+  if (per_lane <= 32) return launch_vpt<T, 32>(logits, M, E, k, renorm, w, ids, stream);
+  const int64_t blocks = (M + kTsWaves - 1) / kTsWaves;
+  hipLaunchKernelGGL((topk_softmax_rows_stream<T>), dim3(int(blocks < 65536 ? blocks : 65536)),
+                     dim3(kTsThreads), 0, stream, static_cast<const T*>(logits), M, E, k, renorm,
+                     w, ids);
+  return hipGetLastError();
 }
 
 }  // namespace
 
-int topk_softmax_max_experts() { return 32 * 64; }
+// Rows beyond 32 * 64 experts take the streaming kernel; ids and indices stay
+// 32-bit.
+int topk_softmax_max_experts() { return 1 << 30; }
 
 int launch_topk_softmax(const void* logits, int dtype, int64_t M, int64_t E, int64_t k,
                         int renorm, float* w, int32_t* ids, hipStream_t stream) {

@@ -158,10 +158,10 @@ def moe_int4_w4a16_hip(A: torch.Tensor, packed: torch.Tensor, scale: torch.Tenso
     ids = _contig(topk_ids, torch.int32)
     tw = _contig(topk_w, torch.float32)
     emap, n_global = _emap(expert_map, dev)
-    nbytes = _lib.query("xk_moe_int4_w4a16_workspace_bytes", M, top_k, E, N, K)
+    nbytes = _lib.query("xk_moe_int4_w4a16_ep_workspace_bytes", M, top_k, E, N, K, n_global)
     if isinstance(workspace, MoeInt4Workspace) and workspace.matches(M, top_k, N, dtype=A.dtype, device=dev):
         out = workspace.out[:M]
-        scratch = workspace.scratch_for(M, E, N, K)
+        scratch = workspace.scratch_for(M, E, N, K, num_global_experts=n_global)
     else:
         out = torch.empty((M, N), dtype=A.dtype, device=dev)
         scratch = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)

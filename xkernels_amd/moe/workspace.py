@@ -110,10 +110,14 @@ class MoeInt4Workspace:
             ws.scratch_for(max_M, num_experts, N, K or 0)
         return ws
 
-    def scratch_for(self, M: int, E: int, N: int, K: int) -> torch.Tensor:
+    def scratch_for(self, M: int, E: int, N: int, K: int, num_global_experts: int = 0) -> torch.Tensor:
+        """The byte buffer for a call with E local experts (of
+        ``num_global_experts`` under an expert map; 0 without one), grown when
+        needed, never shrunk."""
         from .. import _lib
 
-        nbytes = _lib.query("xk_moe_int4_w4a16_workspace_bytes", M, self.top_k, E, N, K)
+        nbytes = _lib.query("xk_moe_int4_w4a16_ep_workspace_bytes", M, self.top_k, E, N, K,
+                            num_global_experts)
         self.scratch = _ensure(self.scratch, nbytes, self.out.device)
         self.num_experts = E
         return self.scratch
