@@ -14,9 +14,14 @@ The same step is also captured once into a HIP graph (``torch.cuda.CUDAGraph``,
 address-stable workspace) and replayed; its time is reported beside the eager
 one as ``ms_per_step_graph`` (``value`` stays the eager rate).
 
-    python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--no-cpu]
+    python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--no-cpu] [--headline-only]
     python bench.py --workload {c3-align,c3-reduce,c4,c5,f1-down,topk-softmax} [--m M]
         (secondary lines)
+
+The default run also times BASELINE configs 3-5 and the down projection (M=64)
+and adds them to the headline line under ``other_configs`` (each with its own
+metric and roofline), and repeats the headline's K steps ``--repeats`` times
+for a min / p10 / p50 / p90 of the per-step time.
 """
 from __future__ import annotations
 
@@ -43,6 +48,10 @@ def parse() -> argparse.Namespace:
                     help="minimum untimed warm work before each timed region (counter passes use 0)")
     ap.add_argument("--gemm-iters", type=int, default=100)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--headline-only", action="store_true",
+                    help="skip the other BASELINE configs in the default run")
+    ap.add_argument("--repeats", type=int, default=10,
+                    help="repeats of the K timed steps for the min / p10 / p90 of the headline")
     ap.add_argument("--seed", type=int, default=20)
     ap.add_argument("--workload", default="c2",
                     choices=["c2", "c3-align", "c3-reduce", "c4", "c5", "f1-down", "topk-softmax"],
@@ -426,6 +435,10 @@ def main() -> int:
     if a.profile_only:
         return 0
 
+    # spread over repeats (the reference's benchmark_repeat reports the min of
+    # repeated means, utils/benchmarking.py:94-141): `value` stays the one
+    # timed region above
+    reps = sorted(_event_time(step, a.steps, 0) for _ in range(max(1, a.repeats)))
     graph_ms = graph_time(step, a.steps, a.warmup)
     gemm_ms = time_gemm_kernel(c, flags, a.gemm_iters)
     achieved = weight_bytes / (gemm_ms * 1e-3) / 1e9
@@ -440,6 +453,9 @@ def main() -> int:
         "ms_per_step": round(ms, 5),
         "us_per_call": round(ms * 1e3, 2),
         "ms_per_step_graph": round(graph_ms, 5),
+        "ms_per_step_repeats": {"n": len(reps), "steps_each": a.steps, "min": round(reps[0], 5),
+                                "p10": round(_pct(reps, 10), 5), "p50": round(_pct(reps, 50), 5),
+                                "p90": round(_pct(reps, 90), 5)},
         "pct_of_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
         "higher_is_better": True,
         "scaling": "weak",
@@ -464,10 +480,44 @@ def main() -> int:
     if t is not None:
         line["roofline"]["traffic"] = t["bytes_per_launch"]
         line["roofline"]["traffic_source"] = str(TRAFFIC_FILE.relative_to(ROOT))
+    if not a.headline_only:
+        line["other_configs"] = other_configs(a)
     if not a.no_cpu:
         line["cpu_baseline"] = cpu_baseline(c)
     print(json.dumps(line))
     return 0
+
+
+def _pct(xs: list[float], q: float) -> float:
+    """q-th percentile of sorted xs (linear interpolation)."""
+    if len(xs) == 1:
+        return xs[0]
+    pos = (len(xs) - 1) * q / 100.0
+    lo = int(pos)
+    hi = min(lo + 1, len(xs) - 1)
+    return xs[lo] + (xs[hi] - xs[lo]) * (pos - lo)
+
+
+# the other BASELINE configs timed by the default run (driver-measured): the
+# secondary line of each
+OTHER_CONFIGS = [("C3-align", "c3-align", {}), ("C3-sum_reduce", "c3-reduce", {}),
+                 ("C4-mxfp4", "c4", {}), ("C5-int4-prefill", "c5", {}),
+                 ("f1-down-M64", "f1-down", {"m": 64})]
+
+
+def other_configs(a) -> dict:
+    import torch
+
+    out = {}
+    for name, workload, extra in OTHER_CONFIGS:
+        sub = argparse.Namespace(**{**vars(a), "workload": workload, "steps": min(a.steps, 20),
+                                    "warmup": min(a.warmup, 5), **extra})
+        t0 = time.perf_counter()
+        r = secondary(sub)
+        r["wall_s"] = round(time.perf_counter() - t0, 2)
+        out[name] = r
+        torch.cuda.empty_cache()
+    return out
 
 
 if __name__ == "__main__":

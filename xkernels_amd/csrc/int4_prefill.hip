@@ -40,16 +40,10 @@ namespace xk {
 namespace {
 
 constexpr int kPBM = 128;              // routed rows per tile
-#ifndef XK_PREFILL_BN
-#define XK_PREFILL_BN 256
-#endif
-constexpr int kPBN = XK_PREFILL_BN;    // output columns per tile
+constexpr int kPBN = 256;              // output columns per tile
 constexpr int kPBK = 128;              // k per pipeline step (4 quantisation groups)
-#ifndef XK_PREFILL_WN
-#define XK_PREFILL_WN 8
-#endif
 constexpr int kWM = 1;                 // waves along the rows
-constexpr int kWN = XK_PREFILL_WN;     // waves along the columns
+constexpr int kWN = 8;                 // waves along the columns
 constexpr int kPWaves = kWM * kWN;
 constexpr int kPThreads = kPWaves * 64;
 constexpr int kStRows = kPThreads / 16;    // activation rows staged per pass
@@ -58,9 +52,6 @@ constexpr int kRT = kPBM / kWM / 16;   // 16-row MFMA tiles per wave
 constexpr int kCT = kPBN / kWN / 16;   // 16-column MFMA tiles per wave
 constexpr int kPStride = kPBK + 16;    // bf16 per LDS row (72 dwords)
 constexpr int kPMaxExperts = 1024;
-#ifndef XK_PREFILL_INTERLEAVE
-#define XK_PREFILL_INTERLEAVE 0
-#endif
 constexpr int kXcds = 8;               // MI355X: 8 XCDs, workgroups round-robin over them
 
 struct PrefillArgs {
@@ -212,18 +203,6 @@ int4_prefill_gemm(PrefillArgs p) {
             acc[i][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], b, acc[i][c], 0, 0, 0);
         }
       }
-#if XK_PREFILL_INTERLEAVE
-      // interleave: each MFMA followed by a few VALU (dequant of later words)
-      // and, every other MFMA, one LDS read
-#pragma unroll
-      for (int m = 0; m < 4 * RT * kCT / 2; ++m) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
-      }
-#endif
     };
 
     u32x4 a0[kSP], a1[kSP], w0[kCT], w1[kCT];
