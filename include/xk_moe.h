@@ -166,6 +166,15 @@ int xk_moe_int4_w4a16_noalloc(const void* A, int32_t a_dtype, int64_t M, int64_t
  * call does this and skips the align). Used by benchmarks to time the GEMM
  * alone. */
 int32_t xk_moe_int4_block_size(int64_t M, int64_t top_k, int64_t E);
+/* Which grouped-GEMM kernel a fused call with these shapes runs: 0 the scalar
+ * kernel (shapes the MFMA kernels do not take), 1 the decode weight-streaming
+ * kernel, 2 the prefill MFMA tile kernel. num_global_experts: the expert map's
+ * size for an expert-parallel call with a workspace of
+ * xk_moe_int4_w4a16_ep_workspace_bytes, else 0. No counterpart in the
+ * reference (its Triton launcher has no such query); for tests and tooling. */
+int32_t xk_moe_int4_kernel(int64_t M, int64_t top_k, int64_t E, int64_t N,
+                           int64_t K, int32_t a_dtype, int32_t group_size,
+                           int32_t flags, int32_t num_global_experts);
 int32_t xk_moe_int4_gemm_parts(int64_t M, int64_t top_k, int64_t E, int64_t N, int64_t K,
                                int32_t a_dtype, int32_t group_size, int32_t flags);
 int64_t xk_moe_int4_gemm_workspace_bytes(int64_t M, int64_t K);

@@ -29,7 +29,7 @@ pytestmark = pytest.mark.gpu
 REL = 2.0 ** -20
 
 
-def _gemm_rows(A, packed, scale, ids, flags=0, self_route=False, emap=None):
+def _gemm_rows(A, packed, scale, ids, flags=0, self_route=False, emap=None, gs=32):
     """fp32 per-slot rows of the grouped GEMM (align with the library's block size,
     or none: the decode kernel then routes the slots itself)."""
     M, K = A.shape
@@ -52,19 +52,19 @@ def _gemm_rows(A, packed, scale, ids, flags=0, self_route=False, emap=None):
     _lib.call("xk_moe_align_block_size", ids.data_ptr(), numel, E, bs, ep, ng, sorted_ids.data_ptr(),
               expert_ids.data_ptr(), num_post.data_ptr(), offsets.data_ptr(), aws.data_ptr(),
               aws.numel(), s)
-    parts = _lib.query("xk_moe_int4_gemm_parts", M, top_k, E, N, K, dt, 32, flags)
+    parts = _lib.query("xk_moe_int4_gemm_parts", M, top_k, E, N, K, dt, gs, flags)
     out = torch.full((parts, numel, N), float("nan"), dtype=torch.float32, device=dev)
     gws = torch.empty(max(256, _lib.query("xk_moe_int4_gemm_workspace_bytes", M, K)), dtype=torch.uint8,
                       device=dev)
     _lib.call("xk_moe_int4_w4a16_gemm", A.data_ptr(), dt, M, K, packed.data_ptr(),
-              scale.data_ptr(), E, N, 32, ids.data_ptr(), top_k, ep, ng,
+              scale.data_ptr(), E, N, gs, ids.data_ptr(), top_k, ep, ng,
               None if self_route else sorted_ids.data_ptr(), None if self_route else offsets.data_ptr(),
               out.data_ptr(), flags, gws.data_ptr(), gws.numel(), s)
     torch.cuda.synchronize()
     return out.sum(0)
 
 
-def _bounded_check(A, packed, scale, ids, rows, rel=REL, w_dtype=torch.bfloat16, emap=None):
+def _bounded_check(A, packed, scale, ids, rows, rel=REL, w_dtype=torch.bfloat16, emap=None, gs=32):
     """Compares every routed slot's row, one expert at a time (float64 reference
     over the weights dequantised to ``w_dtype``: bf16-rounded for bf16
     activations, the exact fp32 products for fp32 ones)."""
@@ -77,7 +77,7 @@ def _bounded_check(A, packed, scale, ids, rows, rel=REL, w_dtype=torch.bfloat16,
         if e < 0:
             continue
         slots = (flat == e).nonzero().reshape(-1)
-        W = dequant_w4a16(packed[e:e + 1], scale[e:e + 1], 32, out_dtype=w_dtype)[0].double()
+        W = dequant_w4a16(packed[e:e + 1], scale[e:e + 1], gs, out_dtype=w_dtype)[0].double()
         a = A[slots // top_k].double()
         want = a @ W.T
         bound = rel * (a.abs() @ W.abs().T) + 1e-30
@@ -88,8 +88,8 @@ def _bounded_check(A, packed, scale, ids, rows, rel=REL, w_dtype=torch.bfloat16,
     return worst
 
 
-def _device_inputs(M, E, N, K, ids, seed):
-    packed, scale, _ = make_w4a16_weights(E, N, K, 32, device="cuda", seed=seed, scale_hi=0.02)
+def _device_inputs(M, E, N, K, ids, seed, gs=32):
+    packed, scale, _ = make_w4a16_weights(E, N, K, gs, device="cuda", seed=seed, scale_hi=0.02)
     g = torch.Generator(device="cuda").manual_seed(seed + 1)
     A = torch.randn(M, K, generator=g, device="cuda").to(torch.bfloat16)
     return A, packed, scale, ids.cuda()
@@ -123,6 +123,40 @@ def test_rows_within_fp32_summation_error(M, E, N, K, top_k, routing):
     rows = _gemm_rows(A, packed, scale, ids)
     assert not torch.isnan(rows).any(), "a routed slot's row was not written"
     _bounded_check(A, packed, scale, ids, rows)
+
+
+KERNEL = {0: "scalar", 1: "stream", 2: "tile"}
+
+
+@pytest.mark.parametrize("M,E,N,K,top_k,gs,routing,kernel", [
+    (64, 48, 4096, 7168, 8, 128, "uniform", "stream"),  # C2 shapes with 128-wide groups
+    (64, 48, 7168, 2048, 8, 64, "uniform", "stream"),   # the down projection, 64-wide groups
+    (1, 16, 256, 1024, 4, 128, "uniform", "stream"),
+    (64, 16, 512, 1024, 4, 64, "zipf", "stream"),       # several 16-row passes per expert
+    (48, 8, 256, 1152, 2, 64, "zipf", "stream"),        # K % 256 != 0: 4-byte scale loads, padded line
+    (40, 6, 160, 1536, 3, 128, "zipf", "stream"),       # 12 scales a row: 4-byte scale loads
+    (1024, 8, 512, 1024, 4, 128, "zipf", "tile"),       # prefill regime
+    (300, 16, 512, 2048, 4, 64, "zipf", "tile"),
+    (16, 8, 512, 1344, 2, 64, "uniform", "scalar"),     # 21 scales a row (odd): the scalar kernel
+])
+def test_group_sizes_64_128_on_mfma_kernels(M, E, N, K, top_k, gs, routing, kernel):
+    """Groups of 64 and 128 run on the MFMA kernels (the decode stream kernel
+    and the prefill tile kernel; the query reports which) and every routed
+    slot's row meets the fp32-summation bound over the bf16-rounded weights of
+    that group size."""
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from xkernels_amd import _lib
+    assert KERNEL[_lib.query("xk_moe_int4_kernel", M, top_k, E, N, K, _lib.XK_DT_BF16, gs, 0, 0)] == kernel
+    ids = uniform_topk(M, top_k, E, 7) if routing == "uniform" else zipf_topk(M, top_k, E, 1.2, 7)
+    print(f"group {gs} M={M} E={E} N={N} K={K} top_k={top_k} {routing} -> {kernel}", flush=True)
+    A, packed, scale, ids = _device_inputs(M, E, N, K, ids, 17, gs=gs)
+    rows = _gemm_rows(A, packed, scale, ids, gs=gs)
+    assert not torch.isnan(rows).any(), "a routed slot's row was not written"
+    _bounded_check(A, packed, scale, ids, rows, gs=gs)
+    if kernel == "stream":  # fp32 activations on the same kernel, exact products
+        rows32 = _gemm_rows(A.float(), packed, scale, ids, gs=gs)
+        _bounded_check(A.float(), packed, scale, ids, rows32, rel=2.0 ** -15, w_dtype=torch.float32, gs=gs)
 
 
 def test_bound_tells_unrounded_weights_apart():

@@ -67,6 +67,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [_p, _i64, _i64, _i64, _p, _i32, _p, _i32, _p, _i32, _p, _i32, _i32, _p],
     ),
     "xk_moe_int4_gemm_parts": (_i32, [_i64, _i64, _i64, _i64, _i64, _i32, _i32, _i32]),
+    "xk_moe_int4_kernel": (_i32, [_i64, _i64, _i64, _i64, _i64, _i32, _i32, _i32, _i32]),
     "xk_moe_mxfp4_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64, _i64]),
     "xk_moe_mxfp4": (
         ctypes.c_int,

@@ -45,6 +45,8 @@ int launch_topk_combine(const float* slot_out, int64_t M, int64_t top_k, int64_t
 int int4_gemm_parts(int64_t M, int64_t top_k, int64_t E, int64_t N, int64_t K, int a_dtype,
                     int group_size, int flags, int64_t ep_global = 0);
 int int4_block_size();
+int int4_kernel_code(int64_t M, int64_t top_k, int64_t E, int64_t N, int64_t K, int a_dtype,
+                     int group_size, int flags, int64_t ep_global);
 bool int4_use_stream(int a_dtype, int group_size, int64_t K);
 bool int4_gemm_self_routes(int64_t M, int64_t top_k, int64_t E, int64_t N, int64_t K, int a_dtype,
                            int group_size, int flags, int64_t ep_global = 0);
@@ -182,6 +184,13 @@ int xk_moe_sum_reduce(const void* y, int32_t y_dtype, int64_t M, int64_t top_k, 
 int32_t xk_moe_int4_block_size(int64_t M, int64_t top_k, int64_t E) {
   (void)M; (void)top_k; (void)E;
   return int4_block_size();
+}
+
+int32_t xk_moe_int4_kernel(int64_t M, int64_t top_k, int64_t E, int64_t N, int64_t K,
+                           int32_t a_dtype, int32_t group_size, int32_t flags,
+                           int32_t num_global_experts) {
+  return int4_kernel_code(M, top_k, E, N, K, a_dtype, group_size, flags,
+                          num_global_experts > E ? num_global_experts : 0);
 }
 
 int32_t xk_moe_int4_gemm_parts(int64_t M, int64_t top_k, int64_t E, int64_t N, int64_t K,

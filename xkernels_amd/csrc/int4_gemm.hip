@@ -76,22 +76,28 @@ int device_cu_count() {
 // Token-slot block size the MFMA kernels consume (one MFMA row tile).
 int int4_block_size() { return 16; }
 
-// The MFMA kernels take 32-wide quantisation groups and bf16 activations
-// (fp32 activations: the weight-streaming kernel only).
+bool int4_rs_group_ok(int64_t K, int group_size);
+
+// The MFMA kernels take quantisation groups of 32, 64 or 128 (an even number
+// of scales per row) and K a multiple of 64; bf16 or fp32 activations (fp32:
+// the weight-streaming kernel only).
 bool int4_use_stream(int a_dtype, int group_size, int64_t K) {
-  return (a_dtype == XK_DT_BF16 || a_dtype == XK_DT_FP32) && group_size == 32 && K % 64 == 0;
+  return (a_dtype == XK_DT_BF16 || a_dtype == XK_DT_FP32) && K % 64 == 0 &&
+         int4_rs_group_ok(K, group_size);
 }
 
 bool int4_prefill_ok(int a_dtype, int group_size, int64_t K, int64_t N, int64_t E);
-bool int4_rs_ok(int64_t M, int64_t top_k, int64_t K, int64_t N, int64_t E, bool f32a);
+bool int4_rs_ok(int64_t M, int64_t top_k, int64_t K, int64_t N, int64_t E, bool f32a,
+                int group_size);
 int int4_rs_slices(int64_t K, int64_t N, int64_t numel, int64_t E, bool f32a);
 bool int4_rs_self_route_ok(int64_t numel);
 int launch_int4_rs(const void* A, bool f32a, int64_t M, int64_t K, const int32_t* packed,
                    const uint16_t* scale, int64_t E, int64_t N, int64_t numel, int64_t top_k,
-                   const int32_t* sorted_ids, const int32_t* offsets, const int32_t* topk_ids,
-                   const int32_t* emap, int num_global, float* slot_out, hipStream_t stream);
+                   int group_size, const int32_t* sorted_ids, const int32_t* offsets,
+                   const int32_t* topk_ids, const int32_t* emap, int num_global, float* slot_out,
+                   hipStream_t stream);
 int launch_int4_prefill(const void* A, int64_t K, const int32_t* packed, const uint16_t* scale,
-                        int64_t E, int64_t N, int64_t numel, int64_t top_k,
+                        int64_t E, int64_t N, int64_t numel, int64_t top_k, int group_size,
                         const int32_t* sorted_ids, const int32_t* offsets, float* slot_out,
                         hipStream_t stream);
 
@@ -127,13 +133,24 @@ Int4Kernel int4_choose(int64_t M, int64_t top_k, int64_t E, int64_t N, int64_t K
   const int64_t local = ep_global > E ? (numel * E + ep_global - 1) / ep_global : numel;
   const bool f32a = a_dtype == XK_DT_FP32;
   const bool tile_ok = !f32a && int4_prefill_ok(a_dtype, group_size, K, N, E);
-  const bool rs_ok = int4_rs_ok(M, top_k, K, N, E, f32a);
+  const bool rs_ok = int4_rs_ok(M, top_k, K, N, E, f32a, group_size);
   bool tile = tile_ok && local >= kPrefillRowsPerExpert * E;
   if (flags & XK_INT4_TEST_FORCE_TILE) tile = tile_ok;
   if (flags & XK_INT4_TEST_FORCE_STREAM) tile = tile && !rs_ok;
   if (tile) return Int4Kernel::kTile;
   if (rs_ok) return Int4Kernel::kRs;
   return tile_ok ? Int4Kernel::kTile : Int4Kernel::kSimple;
+}
+
+// The kernel a call runs, for the C ABI's query: 0 the scalar kernel, 1 the
+// decode stream kernel, 2 the prefill tile kernel.
+int int4_kernel_code(int64_t M, int64_t top_k, int64_t E, int64_t N, int64_t K, int a_dtype,
+                     int group_size, int flags, int64_t ep_global) {
+  switch (int4_choose(M, top_k, E, N, K, a_dtype, group_size, flags, ep_global)) {
+    case Int4Kernel::kRs: return 1;
+    case Int4Kernel::kTile: return 2;
+    default: return 0;
+  }
 }
 
 // Number of fp32 partial planes [parts, M * top_k, N] the grouped GEMM
@@ -186,11 +203,12 @@ int launch_int4_gemm(const void* A, int a_dtype, int64_t M, int64_t K, const int
   }
   switch (kern) {
     case Int4Kernel::kTile:
-      return launch_int4_prefill(A, K, packed, scale, E, N, numel, top_k, sorted_ids, offsets,
-                                 slot_out, stream);
+      return launch_int4_prefill(A, K, packed, scale, E, N, numel, top_k, group_size, sorted_ids,
+                                 offsets, slot_out, stream);
     case Int4Kernel::kRs:
-      return launch_int4_rs(A, a_dtype == XK_DT_FP32, M, K, packed, scale, E, N, numel, top_k, sorted_ids, offsets,
-                            topk_ids, emap, num_global, slot_out, stream);
+      return launch_int4_rs(A, a_dtype == XK_DT_FP32, M, K, packed, scale, E, N, numel, top_k,
+                            group_size, sorted_ids, offsets, topk_ids, emap, num_global, slot_out,
+                            stream);
     case Int4Kernel::kSimple:
       break;
   }

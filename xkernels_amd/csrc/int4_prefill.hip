@@ -57,11 +57,12 @@ constexpr int kXcds = 8;               // MI355X: 8 XCDs, workgroups round-robin
 struct PrefillArgs {
   const uint16_t* A;       // [M, K] bf16
   const uint32_t* packed;  // [E, N, K/8]
-  const uint16_t* scale;   // [E, N, K/32] bf16
+  const uint16_t* scale;   // [E, N, K/g] bf16, g = 32 << glog
   const int32_t* sorted_ids;
   const int32_t* offsets;  // [E+1] padded slot prefix
   float* out;              // [numel, N]
   int K, N, numel, top_k, num_experts;
+  int glog;                // log2(group size / 32)
 };
 
 __global__ void __launch_bounds__(kPThreads)
@@ -74,7 +75,7 @@ int4_prefill_gemm(PrefillArgs p) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int c16 = lane & 15, q = lane >> 4;
   const int wm = wave % kWM, wn = wave / kWM;
-  const int K = p.K, N = p.N, KW = K >> 3, G = K >> 5;
+  const int K = p.K, N = p.N, KW = K >> 3, G = K >> (5 + p.glog);
   const int steps = K / kPBK;
   const int NB = N / kPBN;
   const int E = p.num_experts;
@@ -152,7 +153,7 @@ int4_prefill_gemm(PrefillArgs p) {
     for (int c = 0; c < kCT; ++c) {
       const int64_t n = static_cast<int64_t>(e) * N + n0 + 16 * c + c16;
       wrow[c] = reinterpret_cast<const u32x4*>(p.packed + n * KW) + q;
-      srow[c] = p.scale + n * G + q;
+      srow[c] = p.scale + n * G;
     }
 
     auto load_a = [&](int s, u32x4 (&ar)[kSP]) {
@@ -174,7 +175,7 @@ int4_prefill_gemm(PrefillArgs p) {
 #pragma unroll
       for (int c = 0; c < kCT; ++c) {
         w[c] = wrow[c][s * (kPBK / 32)];
-        sv[c] = srow[c][s * (kPBK / 32)];
+        sv[c] = srow[c][(s * (kPBK / 32) + q) >> p.glog];  // chunk 4 s + q's group
       }
     };
 
@@ -266,18 +267,19 @@ int device_cu_count();
 // Shapes the tile kernel takes: bf16 activations, group 32, K a multiple of two
 // steps, N a multiple of the column tile, at most kPMaxExperts local experts.
 bool int4_prefill_ok(int a_dtype, int group_size, int64_t K, int64_t N, int64_t E) {
-  return a_dtype == XK_DT_BF16 && group_size == 32 && K % (2 * kPBK) == 0 && N % kPBN == 0 &&
-         E <= kPMaxExperts;
+  return a_dtype == XK_DT_BF16 && (group_size == 32 || group_size == 64 || group_size == 128) &&
+         K % (2 * kPBK) == 0 && N % kPBN == 0 && E <= kPMaxExperts;
 }
 
 int launch_int4_prefill(const void* A, int64_t K, const int32_t* packed, const uint16_t* scale,
-                        int64_t E, int64_t N, int64_t numel, int64_t top_k,
+                        int64_t E, int64_t N, int64_t numel, int64_t top_k, int group_size,
                         const int32_t* sorted_ids, const int32_t* offsets, float* slot_out,
                         hipStream_t stream) {
   XK_REQUIRE(reinterpret_cast<uintptr_t>(A) % 16 == 0 && reinterpret_cast<uintptr_t>(packed) % 16 == 0,
              "int4 prefill: A and packed must be 16-byte aligned");
   PrefillArgs a{static_cast<const uint16_t*>(A), reinterpret_cast<const uint32_t*>(packed), scale,
-                sorted_ids, offsets, slot_out, int(K), int(N), int(numel), int(top_k), int(E)};
+                sorted_ids, offsets, slot_out, int(K), int(N), int(numel), int(top_k), int(E),
+                group_size == 128 ? 2 : group_size == 64 ? 1 : 0};
   // one workgroup per CU, a multiple of the XCD count
   const int cus = device_cu_count();
   const int grid = std::max(kXcds, cus / kXcds * kXcds);

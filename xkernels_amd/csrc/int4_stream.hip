@@ -95,6 +95,7 @@ struct RsArgs {
   int a_row_div;            // A row of slot t: t / a_row_div (top_k: token rows; 1: slot rows)
   int slices;               // S: K slices (16 rows x K / S bf16 fit kRsLdsA)
   uint32_t a_bytes;         // bytes of A (buffer resource range)
+  int glog;                 // INT4: log2(group size / 32) (GBIG kernels)
 };
 
 // s_waitcnt vmcnt(n) as a real instruction the compiler accounts for (gfx9
@@ -179,7 +180,11 @@ __device__ __forceinline__ f32x4 quad_transpose(f32x4 e) {
 // 2^-16 of the product): about 2^-15 relative error per term, against the
 // spec's fp32 tolerance of 1e-3. The two activation planes halve the K a
 // slice holds.
-template <int FMT, bool PADK, bool F32A = false>
+// GBIG (INT4): quantisation groups of 64 or 128 (2^glog 32-k chunks share a
+// scale). The block-start scale loads then cover 2^glog lines per 16-byte
+// piece, and each lane reads its chunk's scale from the staged block as one
+// 16-bit LDS read.
+template <int FMT, bool PADK, bool F32A = false, bool GBIG = false>
 __device__ __forceinline__ void stream_body(const RsArgs& p) {
   using F = RsFmt<FMT>;
   constexpr int SB = F::kScaleBytes;
@@ -196,7 +201,8 @@ __device__ __forceinline__ void stream_body(const RsArgs& p) {
   const int wave = uniform(tid >> 6);
 
   const int c16 = lane & 15, q = lane >> 4;
-  const int K = p.K, N = p.N, E = p.E, G = K >> 5, KW = K >> 3;
+  const int glog = GBIG ? p.glog : 0;  // log2(group size / 32)
+  const int K = p.K, N = p.N, E = p.E, G = K >> (5 + glog), KW = K >> 3;
   // K is cut into 256-k lines, the last one zero-padded when K % 256 != 0
   const int S = p.slices, nl = ((K + 255) >> 8) / S, Ks = nl << 8;
   const bool paired = S > 1 && gridDim.x % (8 * S) == 0;
@@ -455,7 +461,7 @@ __device__ __forceinline__ void stream_body(const RsArgs& p) {
     auto issue = [&](Slot& sl) __attribute__((always_inline)) {
       const int cp = my_lo + pi;
       const int wo = cp * 32 * KW * 4 + s * (Ks >> 1) + pl * 128;
-      const int so = cp * 32 * G * SB + (s * (Ks >> 5) + pl * 8) * SB;
+      const int so = cp * 32 * G * SB + ((s * (Ks >> 5) + pl * 8) >> glog) * SB;
       // scales: only on the first line of each block, where lane (c16, q)
       // loads bytes 16 (q + 4 i) .. + 15 of the block's scales (lines pl +
       // (q + 4 i) L .. + L - 1, L = 16-byte loads per line; contiguous bytes
@@ -471,7 +477,9 @@ __device__ __forceinline__ void stream_body(const RsArgs& p) {
 #pragma unroll
           for (int i = 0; i < F::kScLoads; ++i)
           {
-            const int voff = pl + (q + 4 * i) * F::kLinesPerLoad < nl ? s_lane + 16 * (q + 4 * i) : (1 << 30);
+            const int lines = F::kLinesPerLoad << glog;  // lines one 16-byte piece covers
+            const bool in = (q + 4 * i) * lines < kRsScLines && pl + (q + 4 * i) * lines < nl;
+            const int voff = in ? s_lane + 16 * (q + 4 * i) : (1 << 30);
             if constexpr (PADK) {
 #pragma unroll
               for (int d = 0; d < 4; ++d)
@@ -512,7 +520,7 @@ __device__ __forceinline__ void stream_body(const RsArgs& p) {
       uint2 sb[2];     // MXFP4: the line's 8 e8m0 bytes
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
-        if constexpr (FMT == kFmtInt4)
+        if constexpr (FMT == kFmtInt4 && !GBIG)
           sv[c] = sc_lds[wave][c][lb * 16 + c16];
         else
           sb[c] = reinterpret_cast<const uint2*>(&sc_lds[wave][c][0])[((lb >> 1) * 16 + c16) * 2 + (lb & 1)];
@@ -524,7 +532,12 @@ __device__ __forceinline__ void stream_body(const RsArgs& p) {
         bool fnan[2];
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
-          if constexpr (FMT == kFmtInt4) {  // bf16 scale of group 4 h + q -> fp32 (one v_perm_b32)
+          if constexpr (FMT == kFmtInt4 && GBIG) {  // the bf16 scale of chunk 4 h + q's group
+            const int idx = (lb * 8 + 4 * h + q) >> glog;  // scale within the block
+            const uint16_t bits =
+                reinterpret_cast<const uint16_t*>(&sc_lds[wave][c][0])[((idx >> 3) * 16 + c16) * 8 + (idx & 7)];
+            ks[c] = rne_scale(__uint_as_float(uint32_t(bits) << 16));
+          } else if constexpr (FMT == kFmtInt4) {  // bf16 scale of group 4 h + q -> fp32 (one v_perm_b32)
             ks[c] = rne_scale(__uint_as_float(__builtin_amdgcn_perm(sv[c][2 * h + 1], sv[c][2 * h], s_sel)));
           } else {  // e8m0 byte of group 4 h + q: byte q of word h
             const uint32_t b = ((h ? sb[c].y : sb[c].x) >> (8 * q)) & 0xFFu;
@@ -684,6 +697,33 @@ int4_stream_rne_f32_padk(RsArgs p) {
   stream_body<kFmtInt4, true, true>(p);
 }
 
+// Groups of 64 or 128 (scale rows of 16-byte multiples, K a multiple of 256),
+// and the 4-byte-scale-load variants (any even number of scales per row, K a
+// multiple of 64).
+__global__ void __launch_bounds__(kRsThreads)
+__attribute__((amdgpu_waves_per_eu(kRsWaves / 4, kRsWaves / 4)))
+int4_stream_rne_g(RsArgs p) {
+  stream_body<kFmtInt4, false, false, true>(p);
+}
+
+__global__ void __launch_bounds__(kRsThreads)
+__attribute__((amdgpu_waves_per_eu(kRsWaves / 4, kRsWaves / 4)))
+int4_stream_rne_g_padk(RsArgs p) {
+  stream_body<kFmtInt4, true, false, true>(p);
+}
+
+__global__ void __launch_bounds__(kRsThreads)
+__attribute__((amdgpu_waves_per_eu(kRsWaves / 4, kRsWaves / 4)))
+int4_stream_rne_g_f32(RsArgs p) {
+  stream_body<kFmtInt4, false, true, true>(p);
+}
+
+__global__ void __launch_bounds__(kRsThreads)
+__attribute__((amdgpu_waves_per_eu(kRsWaves / 4, kRsWaves / 4)))
+int4_stream_rne_g_f32_padk(RsArgs p) {
+  stream_body<kFmtInt4, true, true, true>(p);
+}
+
 // The same stream over MXFP4 weights (e2m1 nibbles, one e8m0 scale byte per
 // 32-element group: 2^(b - 127), byte 0xFF read as 0): each 8-nibble word
 // becomes 8 bf16 with four v_cvt_scalef32_pk_bf16_fp4 (exact: an e2m1 value
@@ -733,10 +773,20 @@ int mxfp4_rs_slices(int64_t K, int64_t N, int64_t numel, int64_t E) {
   return rs_slices(K, false);
 }
 
-bool int4_rs_ok(int64_t M, int64_t top_k, int64_t K, int64_t N, int64_t E, bool f32a) {
+// Quantisation groups of 32, 64 or 128 whose scale rows are 4-byte multiples
+// (an even number of scales per row; the 16-byte scale loads need 8 per row
+// and K a multiple of 256, else the 4-byte-load variant runs).
+bool int4_rs_group_ok(int64_t K, int group_size) {
+  return (group_size == 32 || group_size == 64 || group_size == 128) && K % group_size == 0 &&
+         (K / group_size) % 2 == 0;
+}
+
+bool int4_rs_ok(int64_t M, int64_t top_k, int64_t K, int64_t N, int64_t E, bool f32a,
+                int group_size) {
   // the last condition: the fp32 partial planes addressable by one buffer resource
   // K % 64: 4-byte aligned scale rows for the padded variant
-  return K % 64 == 0 && N % 32 == 0 && E <= kRsMaxE && rs_slices(K, f32a) > 0 &&
+  return K % 64 == 0 && int4_rs_group_ok(K, group_size) && N % 32 == 0 && E <= kRsMaxE &&
+         rs_slices(K, f32a) > 0 &&
          N * (K / 8) * 4 < (int64_t(1) << 31) && M * K * 4 < (int64_t(1) << 31) &&
          M * top_k * N * 4 * int4_rs_slices(K, N, M * top_k, E, f32a) < (int64_t(1) << 31);
 }
@@ -745,20 +795,26 @@ bool int4_rs_self_route_ok(int64_t numel) { return numel <= kRsMaxSelf; }
 
 int launch_int4_rs(const void* A, bool f32a, int64_t M, int64_t K, const int32_t* packed,
                    const uint16_t* scale, int64_t E, int64_t N, int64_t numel, int64_t top_k,
-                   const int32_t* sorted_ids, const int32_t* offsets, const int32_t* topk_ids,
-                   const int32_t* emap, int num_global, float* slot_out, hipStream_t stream) {
+                   int group_size, const int32_t* sorted_ids, const int32_t* offsets,
+                   const int32_t* topk_ids, const int32_t* emap, int num_global, float* slot_out,
+                   hipStream_t stream) {
+  const int glog = group_size == 128 ? 2 : group_size == 64 ? 1 : 0;
   RsArgs a{static_cast<const uint16_t*>(A), reinterpret_cast<const uint32_t*>(packed), scale,
            sorted_ids, offsets, topk_ids, emap, num_global, slot_out, int(K), int(N), int(E),
            int(numel), int(top_k), int(top_k), int4_rs_slices(K, N, numel, E, f32a),
-           static_cast<uint32_t>(M * K * (f32a ? 4 : 2))};
+           static_cast<uint32_t>(M * K * (f32a ? 4 : 2)), glog};
   const dim3 grid(static_cast<unsigned>(device_cu_count()));
-  const bool padk = K % 256 != 0;
-  if (f32a)
-    hipLaunchKernelGGL(padk ? int4_stream_rne_f32_padk : int4_stream_rne_f32, grid,
-                       dim3(kRsThreads), 0, stream, a);
+  // 4-byte scale loads unless every scale row is a 16-byte multiple and K a
+  // multiple of 256
+  const bool padk = K % 256 != 0 || (K / group_size) % 8 != 0;
+  decltype(&int4_stream_rne) kern;
+  if (glog == 0)
+    kern = f32a ? (padk ? int4_stream_rne_f32_padk : int4_stream_rne_f32)
+                : (padk ? int4_stream_rne_padk : int4_stream_rne);
   else
-    hipLaunchKernelGGL(padk ? int4_stream_rne_padk : int4_stream_rne, grid, dim3(kRsThreads), 0,
-                       stream, a);
+    kern = f32a ? (padk ? int4_stream_rne_g_f32_padk : int4_stream_rne_g_f32)
+                : (padk ? int4_stream_rne_g_padk : int4_stream_rne_g);
+  hipLaunchKernelGGL(kern, grid, dim3(kRsThreads), 0, stream, a);
   XK_CHECK_LAUNCH("int4_stream_rne");
   return XK_OK;
 }
@@ -775,7 +831,7 @@ int launch_mxfp4_rs(const void* A, int64_t a_rows, int64_t K, const uint8_t* w, 
                     const int32_t* emap, int num_global, float* planes, hipStream_t stream) {
   RsArgs a{static_cast<const uint16_t*>(A), reinterpret_cast<const uint32_t*>(w), ws, sorted_ids,
            offsets, topk_ids, emap, num_global, planes, int(K), int(N), int(E), int(numel), 1,
-           int(a_row_div), mxfp4_rs_slices(K, N, numel, E), static_cast<uint32_t>(a_rows * K * 2)};
+           int(a_row_div), mxfp4_rs_slices(K, N, numel, E), static_cast<uint32_t>(a_rows * K * 2), 0};
   if (K % 256 == 0)
     hipLaunchKernelGGL(mxfp4_stream_rs, dim3(static_cast<unsigned>(device_cu_count())),
                        dim3(kRsThreads), 0, stream, a);
