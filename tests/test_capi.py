@@ -169,9 +169,9 @@ def test_int4_ep_workspace_covers_the_expert_parallel_choice():
 
 
 def test_int4_kernel_choice_query():
-    """Groups of 32, 64 and 128 with an even number of scales per row take the
-    MFMA kernels (decode stream below 17 routed rows per expert, prefill tile
-    from there, fp32 activations always the stream kernel); other shapes the
+    """Groups of 32, 64 and 128 take the MFMA kernels (decode stream below 17
+    routed rows per expert, prefill tile from there, fp32 activations always
+    the stream kernel) for K a multiple of 32 and N of 16; other shapes the
     scalar kernel."""
     k = lambda M, top_k, E, N, K, dt, gs, flags=0, ng=0: _lib.query(
         "xk_moe_int4_kernel", M, top_k, E, N, K, dt, gs, flags, ng)
@@ -181,9 +181,11 @@ def test_int4_kernel_choice_query():
         assert k(4096, 8, 48, 4096, 7168, bf, gs) == 2
         assert k(64, 8, 48, 4096, 7168, f32, gs) == 1
     assert k(64, 8, 48, 4096, 7168, bf, 256) == 0        # group size
-    assert k(16, 8, 8, 512, 1344, bf, 64) == 0           # 21 scales a row
+    assert k(16, 8, 8, 512, 1344, bf, 64) == 1           # 21 scales a row (2-byte scale loads)
     assert k(16, 8, 8, 512, 1152, bf, 64) == 1           # 18 scales a row
-    assert k(16, 2, 4, 48, 96, bf, 32) == 0              # K % 64 != 0
+    assert k(16, 2, 4, 48, 96, bf, 32) == 1              # K % 64 != 0, N % 32 != 0 (the spec's sweep point)
+    assert k(16, 2, 4, 40, 96, bf, 32) == 0              # N % 16 != 0
+    assert k(16, 2, 4, 48, 80, bf, 32) == 0              # K % 32 != 0
     assert k(4096, 8, 48, 4096, 7168, bf, 32, _lib._XK_INT4_TEST_FORCE_STREAM) == 1
     assert k(512, 8, 48, 4096, 7168, bf, 32, 0, 0) == 2    # 85 rows per expert
     assert k(512, 8, 48, 4096, 7168, bf, 32, 0, 384) == 1  # 10.7 expected per local expert

@@ -107,7 +107,10 @@ def _device_inputs(M, E, N, K, ids, seed, gs=32):
     (64, 48, 2880, 2880, 8, "uniform"),    # K % 256 != 0: the last 256-k line zero-padded
     (1, 16, 256, 320, 4, "uniform"),       # ... 64 k in the last line
     (200, 8, 256, 1344, 4, "zipf"),        # ... experts with several 16-row passes
-    (16, 8, 512, 2080, 2, "zipf"),         # K % 64 != 0: the scalar kernel
+    (16, 8, 512, 2080, 2, "zipf"),         # K % 64 != 0: 65 scales a row (2-byte scale loads)
+    (37, 8, 48, 96, 3, "zipf"),            # the spec's sweep point: K = 96, N = 48 (a half column pair)
+    (20, 6, 80, 160, 2, "uniform"),        # N % 32 == 16, 5 scales a row
+    (2, 4, 16, 32, 2, "uniform"),          # one 16-column tile, one 32-k group
     (16, 384, 256, 512, 8, "uniform"),     # 384 local experts (the stream kernel takes up to 512)
     (5, 4, 96, 512, 2, "uniform"),         # N not a multiple of 128
     (1024, 8, 512, 1024, 4, "zipf"),       # prefill regime: the MFMA tile kernel
@@ -137,7 +140,8 @@ KERNEL = {0: "scalar", 1: "stream", 2: "tile"}
     (40, 6, 160, 1536, 3, 128, "zipf", "stream"),       # 12 scales a row: 4-byte scale loads
     (1024, 8, 512, 1024, 4, 128, "zipf", "tile"),       # prefill regime
     (300, 16, 512, 2048, 4, 64, "zipf", "tile"),
-    (16, 8, 512, 1344, 2, 64, "uniform", "scalar"),     # 21 scales a row (odd): the scalar kernel
+    (16, 8, 512, 1344, 2, 64, "uniform", "stream"),     # 21 scales a row (odd): 2-byte scale loads
+    (16, 8, 256, 1280, 2, 256, "uniform", "scalar"),    # groups of 256: the scalar kernel
 ])
 def test_group_sizes_64_128_on_mfma_kernels(M, E, N, K, top_k, gs, routing, kernel):
     """Groups of 64 and 128 run on the MFMA kernels (the decode stream kernel
@@ -223,7 +227,10 @@ REL_F32 = 2.0 ** -15
     (1024, 8, 512, 1024, 4, "zipf"),       # prefill regime: fp32 stays on the stream kernel
     (64, 48, 2880, 2880, 8, "uniform"),    # K % 256 != 0: the padded variant
     (1, 16, 256, 320, 4, "uniform"),
-    (16, 8, 512, 2080, 2, "zipf"),         # K % 64 != 0: the scalar kernel
+    (16, 8, 512, 2080, 2, "zipf"),         # K % 64 != 0: 65 scales a row (2-byte scale loads)
+    (37, 8, 48, 96, 3, "zipf"),            # the spec's sweep point: K = 96, N = 48 (a half column pair)
+    (20, 6, 80, 160, 2, "uniform"),        # N % 32 == 16, 5 scales a row
+    (2, 4, 16, 32, 2, "uniform"),          # one 16-column tile, one 32-k group
     (16, 384, 256, 512, 8, "uniform"),     # 384 local experts
 ])
 def test_fp32_rows_within_split_error(M, E, N, K, top_k, routing):

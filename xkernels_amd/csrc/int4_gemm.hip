@@ -78,11 +78,10 @@ int int4_block_size() { return 16; }
 
 bool int4_rs_group_ok(int64_t K, int group_size);
 
-// The MFMA kernels take quantisation groups of 32, 64 or 128 (an even number
-// of scales per row) and K a multiple of 64; bf16 or fp32 activations (fp32:
-// the weight-streaming kernel only).
+// The MFMA kernels take quantisation groups of 32, 64 or 128 and K a multiple
+// of 32; bf16 or fp32 activations (fp32: the weight-streaming kernel only).
 bool int4_use_stream(int a_dtype, int group_size, int64_t K) {
-  return (a_dtype == XK_DT_BF16 || a_dtype == XK_DT_FP32) && K % 64 == 0 &&
+  return (a_dtype == XK_DT_BF16 || a_dtype == XK_DT_FP32) && K % 32 == 0 &&
          int4_rs_group_ok(K, group_size);
 }
 

@@ -168,11 +168,12 @@ __device__ __forceinline__ f32x4 quad_transpose(f32x4 e) {
   return e;
 }
 
-// PADK: K is not a multiple of 256 (the last line zero-padded). The scale
-// rows are then not 16-byte multiples, so the block-start scale loads are
-// 4-byte loads: each lies wholly inside or wholly past the buffer (a 16-byte
-// load that straddles the end of the scales comes back empty, real bytes
-// included), and needs only 4-byte alignment of the rows.
+// SLD: bytes per block-start scale load. 16 when K is a multiple of 256 and
+// every scale row a 16-byte multiple; else (PADK) 4-byte loads, or 2-byte ones
+// for an odd number of scales per row: each lies wholly inside or wholly past
+// the buffer (a 16-byte load that straddles the end of the scales comes back
+// empty, real bytes included) and needs only 4- (2-) byte aligned rows. K not
+// a multiple of 256 zero-pads the last line's activations.
 // F32A (INT4 only): fp32 activations, whose reference contraction uses the
 // exact products (n - 8) s. The activations are staged as a bf16 pair hi + lo
 // (A - hi - lo <= 2^-16 |A|), the weights split exactly (dequant_split_nat),
@@ -184,8 +185,9 @@ __device__ __forceinline__ f32x4 quad_transpose(f32x4 e) {
 // scale). The block-start scale loads then cover 2^glog lines per 16-byte
 // piece, and each lane reads its chunk's scale from the staged block as one
 // 16-bit LDS read.
-template <int FMT, bool PADK, bool F32A = false, bool GBIG = false>
+template <int FMT, int SLD, bool F32A = false, bool GBIG = false>
 __device__ __forceinline__ void stream_body(const RsArgs& p) {
+  constexpr bool PADK = SLD != 16;
   using F = RsFmt<FMT>;
   constexpr int SB = F::kScaleBytes;
   __shared__ __attribute__((aligned(16))) u32x4 a_lds[kRsLdsA / 16];
@@ -206,7 +208,7 @@ __device__ __forceinline__ void stream_body(const RsArgs& p) {
   // K is cut into 256-k lines, the last one zero-padded when K % 256 != 0
   const int S = p.slices, nl = ((K + 255) >> 8) / S, Ks = nl << 8;
   const bool paired = S > 1 && gridDim.x % (8 * S) == 0;
-  const int ncp = N >> 5;            // column pairs per expert
+  const int ncp = (N + 31) >> 5;     // column pairs per expert (N % 32 == 16: the last one half)
   const int nblk = nl * 8;           // 1 KiB operand blocks of one activation slice
   const uint32_t kNibMask = in_vgpr(0x000F000Fu), kNibMaskHi = in_vgpr(0x00F000F0u);
 
@@ -421,6 +423,9 @@ __device__ __forceinline__ void stream_body(const RsArgs& p) {
   const int qb = lane & 3, qa = (lane >> 2) & 3;  // c16 = 4 qa + qb
   f32x4 keep[kRsKeep][2];
   uint32_t keep_off[kRsKeep];
+  // bit i: kept pair i's second 16-column tile lies inside N (N % 32 == 16
+  // runs the PADK variants, which keep this mask)
+  uint32_t keep_t1 = 0;
   int nkeep = 0;  // wave-uniform
   auto write_kept = [&]() __attribute__((always_inline)) {
     static_for<kRsKeep>([&](auto I) {
@@ -428,8 +433,9 @@ __device__ __forceinline__ void stream_body(const RsArgs& p) {
         const f32x4 d0 = quad_transpose(keep[I][0]), d1 = quad_transpose(keep[I][1]);
         __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, d0), ro, keep_off[I], 0,
                                                kRsStorePolicy);
-        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, d1), ro, keep_off[I] + 64, 0,
-                                               kRsStorePolicy);
+        if (!PADK || ((keep_t1 >> decltype(I)::value) & 1u))
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, d1), ro, keep_off[I] + 64, 0,
+                                                 kRsStorePolicy);
       }
     });
     nkeep = 0;
@@ -480,7 +486,14 @@ __device__ __forceinline__ void stream_body(const RsArgs& p) {
             const int lines = F::kLinesPerLoad << glog;  // lines one 16-byte piece covers
             const bool in = (q + 4 * i) * lines < kRsScLines && pl + (q + 4 * i) * lines < nl;
             const int voff = in ? s_lane + 16 * (q + 4 * i) : (1 << 30);
-            if constexpr (PADK) {
+            if constexpr (SLD == 2) {
+#pragma unroll
+              for (int d = 0; d < 4; ++d) {
+                const uint32_t lo = __builtin_amdgcn_raw_buffer_load_b16(rs, voff + 4 * d, so + c * 16 * G * SB, 0);
+                const uint32_t hi = __builtin_amdgcn_raw_buffer_load_b16(rs, voff + 4 * d + 2, so + c * 16 * G * SB, 0);
+                sl.s[c][i][d] = lo | (hi << 16);
+              }
+            } else if constexpr (SLD == 4) {
 #pragma unroll
               for (int d = 0; d < 4; ++d)
                 sl.s[c][i][d] = __builtin_amdgcn_raw_buffer_load_b32(rs, voff + 4 * d, so + c * 16 * G * SB,
@@ -587,6 +600,9 @@ __device__ __forceinline__ void stream_body(const RsArgs& p) {
           keep[I][0] = acc[0];
           keep[I][1] = acc[1];
           keep_off[I] = off;
+          if constexpr (PADK)
+            keep_t1 = (keep_t1 & ~(1u << decltype(I)::value)) |
+                      (((my_lo + i) * 32 + 16 < N ? 1u : 0u) << decltype(I)::value);
         }
       });
       ++nkeep;
@@ -674,27 +690,27 @@ __device__ __forceinline__ void stream_body(const RsArgs& p) {
 __global__ void __launch_bounds__(kRsThreads)
 __attribute__((amdgpu_waves_per_eu(kRsWaves / 4, kRsWaves / 4)))
 int4_stream_rne(RsArgs p) {
-  stream_body<kFmtInt4, false>(p);
+  stream_body<kFmtInt4, 16>(p);
 }
 
 // K not a multiple of 256 (a multiple of 64: 4-byte scale rows).
 __global__ void __launch_bounds__(kRsThreads)
 __attribute__((amdgpu_waves_per_eu(kRsWaves / 4, kRsWaves / 4)))
 int4_stream_rne_padk(RsArgs p) {
-  stream_body<kFmtInt4, true>(p);
+  stream_body<kFmtInt4, 4>(p);
 }
 
 // fp32 activations (K a multiple of 256, and the padded variant).
 __global__ void __launch_bounds__(kRsThreads)
 __attribute__((amdgpu_waves_per_eu(kRsWaves / 4, kRsWaves / 4)))
 int4_stream_rne_f32(RsArgs p) {
-  stream_body<kFmtInt4, false, true>(p);
+  stream_body<kFmtInt4, 16, true>(p);
 }
 
 __global__ void __launch_bounds__(kRsThreads)
 __attribute__((amdgpu_waves_per_eu(kRsWaves / 4, kRsWaves / 4)))
 int4_stream_rne_f32_padk(RsArgs p) {
-  stream_body<kFmtInt4, true, true>(p);
+  stream_body<kFmtInt4, 4, true>(p);
 }
 
 // Groups of 64 or 128 (scale rows of 16-byte multiples, K a multiple of 256),
@@ -703,25 +719,50 @@ int4_stream_rne_f32_padk(RsArgs p) {
 __global__ void __launch_bounds__(kRsThreads)
 __attribute__((amdgpu_waves_per_eu(kRsWaves / 4, kRsWaves / 4)))
 int4_stream_rne_g(RsArgs p) {
-  stream_body<kFmtInt4, false, false, true>(p);
+  stream_body<kFmtInt4, 16, false, true>(p);
 }
 
 __global__ void __launch_bounds__(kRsThreads)
 __attribute__((amdgpu_waves_per_eu(kRsWaves / 4, kRsWaves / 4)))
 int4_stream_rne_g_padk(RsArgs p) {
-  stream_body<kFmtInt4, true, false, true>(p);
+  stream_body<kFmtInt4, 4, false, true>(p);
 }
 
 __global__ void __launch_bounds__(kRsThreads)
 __attribute__((amdgpu_waves_per_eu(kRsWaves / 4, kRsWaves / 4)))
 int4_stream_rne_g_f32(RsArgs p) {
-  stream_body<kFmtInt4, false, true, true>(p);
+  stream_body<kFmtInt4, 16, true, true>(p);
 }
 
 __global__ void __launch_bounds__(kRsThreads)
 __attribute__((amdgpu_waves_per_eu(kRsWaves / 4, kRsWaves / 4)))
 int4_stream_rne_g_f32_padk(RsArgs p) {
-  stream_body<kFmtInt4, true, true, true>(p);
+  stream_body<kFmtInt4, 4, true, true>(p);
+}
+
+// An odd number of scales per row: 2-byte scale loads (K a multiple of 32).
+__global__ void __launch_bounds__(kRsThreads)
+__attribute__((amdgpu_waves_per_eu(kRsWaves / 4, kRsWaves / 4)))
+int4_stream_rne_sld2(RsArgs p) {
+  stream_body<kFmtInt4, 2>(p);
+}
+
+__global__ void __launch_bounds__(kRsThreads)
+__attribute__((amdgpu_waves_per_eu(kRsWaves / 4, kRsWaves / 4)))
+int4_stream_rne_f32_sld2(RsArgs p) {
+  stream_body<kFmtInt4, 2, true>(p);
+}
+
+__global__ void __launch_bounds__(kRsThreads)
+__attribute__((amdgpu_waves_per_eu(kRsWaves / 4, kRsWaves / 4)))
+int4_stream_rne_g_sld2(RsArgs p) {
+  stream_body<kFmtInt4, 2, false, true>(p);
+}
+
+__global__ void __launch_bounds__(kRsThreads)
+__attribute__((amdgpu_waves_per_eu(kRsWaves / 4, kRsWaves / 4)))
+int4_stream_rne_g_f32_sld2(RsArgs p) {
+  stream_body<kFmtInt4, 2, true, true>(p);
 }
 
 // The same stream over MXFP4 weights (e2m1 nibbles, one e8m0 scale byte per
@@ -732,14 +773,14 @@ int4_stream_rne_g_f32_padk(RsArgs p) {
 __global__ void __launch_bounds__(kRsThreads)
 __attribute__((amdgpu_waves_per_eu(kRsWaves / 4, kRsWaves / 4)))
 mxfp4_stream_rs(RsArgs p) {
-  stream_body<kFmtFp4, false>(p);
+  stream_body<kFmtFp4, 16>(p);
 }
 
 // K not a multiple of 256 (a multiple of 128: 4-byte scale rows).
 __global__ void __launch_bounds__(kRsThreads)
 __attribute__((amdgpu_waves_per_eu(kRsWaves / 4, kRsWaves / 4)))
 mxfp4_stream_rs_padk(RsArgs p) {
-  stream_body<kFmtFp4, true>(p);
+  stream_body<kFmtFp4, 4>(p);
 }
 
 }  // namespace
@@ -773,19 +814,17 @@ int mxfp4_rs_slices(int64_t K, int64_t N, int64_t numel, int64_t E) {
   return rs_slices(K, false);
 }
 
-// Quantisation groups of 32, 64 or 128 whose scale rows are 4-byte multiples
-// (an even number of scales per row; the 16-byte scale loads need 8 per row
-// and K a multiple of 256, else the 4-byte-load variant runs).
+// Quantisation groups of 32, 64 or 128 (the 16-byte scale loads need 8
+// scales per row and K a multiple of 256; else 4-byte loads for an even
+// number of scales per row, 2-byte loads for an odd one).
 bool int4_rs_group_ok(int64_t K, int group_size) {
-  return (group_size == 32 || group_size == 64 || group_size == 128) && K % group_size == 0 &&
-         (K / group_size) % 2 == 0;
+  return (group_size == 32 || group_size == 64 || group_size == 128) && K % group_size == 0;
 }
 
 bool int4_rs_ok(int64_t M, int64_t top_k, int64_t K, int64_t N, int64_t E, bool f32a,
                 int group_size) {
   // the last condition: the fp32 partial planes addressable by one buffer resource
-  // K % 64: 4-byte aligned scale rows for the padded variant
-  return K % 64 == 0 && int4_rs_group_ok(K, group_size) && N % 32 == 0 && E <= kRsMaxE &&
+  return K % 32 == 0 && int4_rs_group_ok(K, group_size) && N % 16 == 0 && E <= kRsMaxE &&
          rs_slices(K, f32a) > 0 &&
          N * (K / 8) * 4 < (int64_t(1) << 31) && M * K * 4 < (int64_t(1) << 31) &&
          M * top_k * N * 4 * int4_rs_slices(K, N, M * top_k, E, f32a) < (int64_t(1) << 31);
@@ -804,16 +843,17 @@ int launch_int4_rs(const void* A, bool f32a, int64_t M, int64_t K, const int32_t
            int(numel), int(top_k), int(top_k), int4_rs_slices(K, N, numel, E, f32a),
            static_cast<uint32_t>(M * K * (f32a ? 4 : 2)), glog};
   const dim3 grid(static_cast<unsigned>(device_cu_count()));
-  // 4-byte scale loads unless every scale row is a 16-byte multiple and K a
-  // multiple of 256
-  const bool padk = K % 256 != 0 || (K / group_size) % 8 != 0;
+  // 16-byte scale loads when every scale row is a 16-byte multiple and K a
+  // multiple of 256, else 4-byte (even scale count per row) or 2-byte ones
+  const int64_t G = K / group_size;
+  const int sld = K % 256 == 0 && G % 8 == 0 && N % 32 == 0 ? 16 : G % 2 == 0 ? 4 : 2;
   decltype(&int4_stream_rne) kern;
   if (glog == 0)
-    kern = f32a ? (padk ? int4_stream_rne_f32_padk : int4_stream_rne_f32)
-                : (padk ? int4_stream_rne_padk : int4_stream_rne);
+    kern = f32a ? (sld == 16 ? int4_stream_rne_f32 : sld == 4 ? int4_stream_rne_f32_padk : int4_stream_rne_f32_sld2)
+                : (sld == 16 ? int4_stream_rne : sld == 4 ? int4_stream_rne_padk : int4_stream_rne_sld2);
   else
-    kern = f32a ? (padk ? int4_stream_rne_g_f32_padk : int4_stream_rne_g_f32)
-                : (padk ? int4_stream_rne_g_padk : int4_stream_rne_g);
+    kern = f32a ? (sld == 16 ? int4_stream_rne_g_f32 : sld == 4 ? int4_stream_rne_g_f32_padk : int4_stream_rne_g_f32_sld2)
+                : (sld == 16 ? int4_stream_rne_g : sld == 4 ? int4_stream_rne_g_padk : int4_stream_rne_g_sld2);
   hipLaunchKernelGGL(kern, grid, dim3(kRsThreads), 0, stream, a);
   XK_CHECK_LAUNCH("int4_stream_rne");
   return XK_OK;
