@@ -7,8 +7,8 @@
 // (every load instruction of the wave reads one contiguous run of logits), so a
 // row of E experts sits in VPT = ceil(E/64) (rounded to a power of two)
 // registers per lane. Max and sum are wave reductions; each of the k rounds
-// picks the wave-wide best (probability, -id) among the experts not yet taken
-// with one xor-shuffle butterfly, and the lane holding the winner marks it.
+// takes the wave-wide largest (probability, -id) key below the previous
+// round's winner with one xor-shuffle butterfly.
 // Selections are staged in LDS so the renormalisation and the [M, k] output
 // writes are contiguous across lanes.
 //
@@ -39,16 +39,36 @@ __device__ __forceinline__ float logit_at<float>(const float* p) {
   return *p;
 }
 
-// a ranks before b in the reference's stable descending sort (torch.sort,
-// topk_softmax.py:88): NaN above every number, then larger probability; equal
-// keys (NaN and NaN included) to the lower id. A row with a NaN or +inf logit,
+// The reference's stable descending sort (torch.sort, topk_softmax.py:88)
+// orders experts by probability, NaN above every number, and equal keys (NaN
+// and NaN included) by lower id. One 64-bit key per expert encodes that order
+// as an unsigned integer order: the high word is 0xFFFFFFFE for NaN and the
+// probability's bit pattern + 1 otherwise (probabilities are +0 .. 1, whose
+// bit patterns are ordered like the values; 0 is left for padding), the low
+// word ~id (a lower id gives the larger key). Keys are unique and below
+// ~0 (round 0's bound), so round t's winner is the largest key below round
+// t-1's. A row with a NaN or +inf logit,
 // or only -inf logits, softmaxes to all NaN (as torch's does: the NaN or the
 // inf - inf reaches the sum), so it selects experts 0 .. k-1 with NaN weights.
-__device__ __forceinline__ bool ranks_before(float a, int ia, float b, int ib) {
-  const bool an = __builtin_isnan(a), bn = __builtin_isnan(b);
-  if (an != bn) return an;
-  if (an) return ia < ib;
-  return a > b || (a == b && ia < ib);
+__device__ __forceinline__ uint64_t rank_key(float p, int e) {
+  const uint32_t hi = __builtin_isnan(p) ? 0xFFFFFFFEu : __float_as_uint(p) + 1u;
+  return (uint64_t(hi) << 32) | uint32_t(~e);
+}
+__device__ __forceinline__ float key_prob(uint64_t key) {
+  const uint32_t hi = uint32_t(key >> 32);
+  return hi == 0xFFFFFFFEu ? __builtin_nanf("") : __uint_as_float(hi - 1u);
+}
+__device__ __forceinline__ int key_id(uint64_t key) { return int(~uint32_t(key)); }
+
+// Largest key of the wave.
+__device__ __forceinline__ uint64_t wave_max_key(uint64_t b) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const uint32_t lo = __shfl_xor(uint32_t(b), off), hi = __shfl_xor(uint32_t(b >> 32), off);
+    const uint64_t o = (uint64_t(hi) << 32) | lo;
+    b = o > b ? o : b;
+  }
+  return b;
 }
 
 template <typename T, int VPT>
@@ -83,38 +103,23 @@ topk_softmax_rows(const T* __restrict__ logits, int64_t M, int E, int k, int ren
     }
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) sum += __shfl_xor(sum, off);
+    uint64_t key[VPT];
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
       const int e = j * 64 + lane;
-      p[j] = e < E ? p[j] / sum : -1.f;  // padding never ranks above a real expert
+      key[j] = e < E ? rank_key(p[j] / sum, e) : 0;  // padding ranks below every expert
     }
 
-    uint32_t taken = 0;
     float picked_sum = 0.f;
+    uint64_t prev = ~uint64_t(0);
     for (int t = 0; t < k; ++t) {
-      float bv = -2.f;
-      int bid = 0x7fffffff;
+      uint64_t best = 0;
 #pragma unroll
-      for (int j = 0; j < VPT; ++j) {
-        const int e = j * 64 + lane;
-        if (!((taken >> j) & 1u) && ranks_before(p[j], e, bv, bid)) {
-          bv = p[j];
-          bid = e;
-        }
-      }
-#pragma unroll
-      for (int off = 32; off >= 1; off >>= 1) {
-        const float ov = __shfl_xor(bv, off);
-        const int oid = __shfl_xor(bid, off);
-        if (ranks_before(ov, oid, bv, bid)) {
-          bv = ov;
-          bid = oid;
-        }
-      }
-      // every lane now holds the same winner (bv, bid)
-      // (the winner is a real expert: k <= E, and every expert ranks before
-      // the padding's -1)
-      if (lane == (bid & 63) && (bid >> 6) < VPT) taken |= 1u << (bid >> 6);
+      for (int j = 0; j < VPT; ++j) best = key[j] < prev && key[j] > best ? key[j] : best;
+      // every lane now holds the same winner (k <= E: a real expert)
+      prev = wave_max_key(best);
+      const float bv = key_prob(prev);
+      const int bid = key_id(prev);
       if (lane == 0) {
         sel_w[t] = bv;
         sel_id[t] = bid;
@@ -136,11 +141,10 @@ topk_softmax_rows(const T* __restrict__ logits, int64_t M, int E, int k, int ren
 }
 
 // Rows of more than 32 * 64 experts: the same selection without holding the
-// row in registers. Round t re-reads the row (from L2) and takes the best
-// expert that ranks after round t-1's winner (the ranking is a total order,
-// so no taken-set is needed): k * E reads and exponentials per row. The lane
-// t % 64 writes the t-th selection; the renormalisation then rescales each
-// lane's own writes.
+// row in registers. Round t re-reads the row (from L2) and takes the largest
+// key below round t-1's winner (the same keys as above): k * E reads and
+// exponentials per row. The lane t % 64 writes the t-th selection; the
+// renormalisation then rescales each lane's own writes.
 template <typename T>
 __global__ void __launch_bounds__(kTsThreads)
 topk_softmax_rows_stream(const T* __restrict__ logits, int64_t M, int E, int k, int renorm,
@@ -158,34 +162,22 @@ topk_softmax_rows_stream(const T* __restrict__ logits, int64_t M, int E, int k, 
     for (int e = lane; e < E; e += 64) sum += expf(logit_at<T>(g + e) - mx);
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) sum += __shfl_xor(sum, off);
-    float pv = 0.f, picked_sum = 0.f;
-    int pid = -1;  // no previous winner
+    float picked_sum = 0.f;
+    uint64_t prev = ~uint64_t(0);
     for (int t = 0; t < k; ++t) {
-      float bv = -2.f;
-      int bid = 0x7fffffff;
+      uint64_t best = 0;
       for (int e = lane; e < E; e += 64) {
-        const float v = expf(logit_at<T>(g + e) - mx) / sum;
-        if ((pid < 0 || ranks_before(pv, pid, v, e)) && ranks_before(v, e, bv, bid)) {
-          bv = v;
-          bid = e;
-        }
+        const uint64_t v = rank_key(expf(logit_at<T>(g + e) - mx) / sum, e);
+        best = v < prev && v > best ? v : best;
       }
-#pragma unroll
-      for (int off = 32; off >= 1; off >>= 1) {
-        const float ov = __shfl_xor(bv, off);
-        const int oid = __shfl_xor(bid, off);
-        if (ranks_before(ov, oid, bv, bid)) {
-          bv = ov;
-          bid = oid;
-        }
-      }
+      prev = wave_max_key(best);
+      const float bv = key_prob(prev);
+      const int bid = key_id(prev);
       if (lane == (t & 63)) {
         w_out[row * k + t] = bv;
         id_out[row * k + t] = bid;
       }
       picked_sum += bv;
-      pv = bv;
-      pid = bid;
     }
     if (renorm)
       for (int t = lane; t < k; t += 64) w_out[row * k + t] = w_out[row * k + t] / picked_sum;
