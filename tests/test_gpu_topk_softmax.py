@@ -3,9 +3,11 @@
 ids must match exactly, including the ascending-id order of tied
 probabilities (bf16/fp16 logits tie often); weights within the Op Spec's
 per-dtype tolerance. Cases follow the reference's tests/test_topk_softmax.py
-(:88-116) plus the edges of this kernel: E not a multiple of 64, E at its
-2048 limit, k = E, k > 64, rows with many exact ties and with probabilities
-that underflow to 0, and the reference's measured shape (M=4096, E=256, k=8).
+(:88-116) plus the edges of this kernel: E not a multiple of 64, E = 2048 (the
+largest register-resident row) and above it (the streaming kernel), k = E,
+k > 64, rows with many exact ties, with probabilities that underflow to 0 and
+with NaN / +-inf logits, and the reference's measured shape (M=4096, E=256,
+k=8).
 """
 from __future__ import annotations
 
