@@ -124,4 +124,25 @@ __device__ __forceinline__ bf16x8 fp4x8_to_bf16(uint32_t w, float s) {
   return r;
 }
 
+// The MXFP4 MoE's clamped SwiGLU of one column j of a slot (mxfp4_reference.py,
+// gu = bf16(A @ w13^T) (+ b13 -> bf16), act = bf16(silu(min(g, L)) *
+// clamp(u, -L, L))): g and u are the fp32 sums of gate column j and up column
+// ispp + j, b13e the expert's bias row (nullable), limit <= 0 no clamp. Every
+// kernel that finishes the gate/up projection calls this, so they agree bit
+// for bit.
+__device__ __forceinline__ uint16_t mxfp4_swiglu(float g, float u, const uint16_t* b13e, int j,
+                                                 int ispp, float limit) {
+  g = round_bf16(g);
+  u = round_bf16(u);
+  if (b13e != nullptr) {
+    g = round_bf16(g + bf16_to_f32(b13e[j]));
+    u = round_bf16(u + bf16_to_f32(b13e[ispp + j]));
+  }
+  if (limit > 0.f) {
+    g = fminf(g, limit);
+    u = fminf(fmaxf(u, -limit), limit);
+  }
+  return f32_to_bf16((g / (1.0f + __expf(-g))) * u);
+}
+
 }  // namespace xk

@@ -209,19 +209,9 @@ mxfp4_stream_gemm(Mxfp4Args p) {
         if (STAGE == 0) {
           const int j = col[0];
           if (j >= p.ncols) continue;
-          float g = round_bf16(acc[t][0][i]);
-          float u = round_bf16(acc[t][1][i]);
-          if (p.bias != nullptr) {
-            const uint16_t* b = p.bias + static_cast<int64_t>(e) * 2 * p.ncols;
-            g = round_bf16(g + bf16_to_f32(b[j]));
-            u = round_bf16(u + bf16_to_f32(b[p.ncols + j]));
-          }
-          if (p.limit > 0.f) {
-            g = fminf(g, p.limit);
-            u = fminf(fmaxf(u, -p.limit), p.limit);
-          }
-          const float a = (g / (1.0f + __expf(-g))) * u;
-          p.act[static_cast<int64_t>(slot) * p.ncols + j] = f32_to_bf16(a);
+          const uint16_t* b = p.bias ? p.bias + static_cast<int64_t>(e) * 2 * p.ncols : nullptr;
+          p.act[static_cast<int64_t>(slot) * p.ncols + j] =
+              mxfp4_swiglu(acc[t][0][i], acc[t][1][i], b, j, p.ncols, p.limit);
         } else {
 #pragma unroll
           for (int c = 0; c < 2; ++c) {
@@ -280,20 +270,9 @@ mxfp4_swiglu_planes(const float* __restrict__ planes, int S, int64_t numel, int 
     u += *reinterpret_cast<const f32x4*>(row + sl * pstride + ispp + j0);
   }
   uint16_t r[4];
+  const uint16_t* b = b13 ? b13 + static_cast<int64_t>(e) * 2 * ispp : nullptr;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    float gv = round_bf16(g[i]), uv = round_bf16(u[i]);
-    if (b13 != nullptr) {
-      const uint16_t* b = b13 + static_cast<int64_t>(e) * 2 * ispp;
-      gv = round_bf16(gv + bf16_to_f32(b[j0 + i]));
-      uv = round_bf16(uv + bf16_to_f32(b[ispp + j0 + i]));
-    }
-    if (limit > 0.f) {
-      gv = fminf(gv, limit);
-      uv = fminf(fmaxf(uv, -limit), limit);
-    }
-    r[i] = f32_to_bf16((gv / (1.0f + __expf(-gv))) * uv);
-  }
+  for (int i = 0; i < 4; ++i) r[i] = mxfp4_swiglu(g[i], u[i], b, j0 + i, ispp, limit);
   uint2 o;
   o.x = r[0] | (static_cast<uint32_t>(r[1]) << 16);
   o.y = r[2] | (static_cast<uint32_t>(r[3]) << 16);
