@@ -457,9 +457,9 @@ __device__ __forceinline__ void stream_body(const RsArgs& p) {
 
   auto run_chunk = [&](int e, int s, int my_lo, int cnt) __attribute__((always_inline)) {
     if (cnt == 0) return;
-    // a chunk adds at most kRsMaxCp pairs: room is made before its stream
-    // starts, so the step loop below never stores
-    if (nkeep > kRsKeep - kRsMaxCp) write_kept();
+    // the chunk's cnt <= kRsMaxCp pairs join the kept ones: room is made
+    // before its stream starts, so the step loop below never stores
+    if (nkeep + cnt > kRsKeep) write_kept();
     const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint32_t*>(p.packed + static_cast<int64_t>(e) * N * KW), 0, N * KW * 4, 0x00020000);
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
