@@ -45,11 +45,11 @@ __device__ __forceinline__ float logit_at<float>(const float* p) {
 // as an unsigned integer order: the high word is 0xFFFFFFFE for NaN and the
 // probability's bit pattern + 1 otherwise (probabilities are +0 .. 1, whose
 // bit patterns are ordered like the values; 0 is left for padding), the low
-// word ~id (a lower id gives the larger key). Keys are unique and below
-// ~0 (round 0's bound), so round t's winner is the largest key below round
-// t-1's. A row with a NaN or +inf logit,
-// or only -inf logits, softmaxes to all NaN (as torch's does: the NaN or the
-// inf - inf reaches the sum), so it selects experts 0 .. k-1 with NaN weights.
+// word ~id (a lower id gives the larger key). Keys are unique and below ~0,
+// the bound of the first selection, so selection t takes the largest key
+// below selection t-1's. A row with a NaN or +inf logit, or only -inf
+// logits, softmaxes to all NaN (as torch's does: the NaN or the inf - inf
+// reaches the sum), so it selects experts 0 .. k-1 with NaN weights.
 __device__ __forceinline__ uint64_t rank_key(float p, int e) {
   const uint32_t hi = __builtin_isnan(p) ? 0xFFFFFFFEu : __float_as_uint(p) + 1u;
   return (uint64_t(hi) << 32) | uint32_t(~e);
