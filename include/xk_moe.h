@@ -157,8 +157,10 @@ int xk_moe_int4_w4a16_noalloc(const void* A, int32_t a_dtype, int64_t M, int64_t
  * untouched). The decode kernel splits K: slot_out is [parts, numel, N] with
  * parts = xk_moe_int4_gemm_parts(...) for the same arguments; every plane
  * holds one K slice's partial rows and xk_moe_topk_combine(..., nparts =
- * parts) sums them. The kernels need no workspace: xk_moe_int4_gemm_workspace_bytes
- * returns 0 and the workspace argument may be NULL. A, packed and scale
+ * parts) sums them. The prefill tile kernel keeps a tile queue of
+ * xk_moe_int4_gemm_workspace_bytes(...) bytes in the workspace (one workspace
+ * per concurrently running call); with a NULL or smaller workspace it deals
+ * its tiles statically. The other kernels use no workspace. A, packed and scale
  * must be 16-byte aligned for the MFMA kernels. In the decode regime
  * (xk_moe_int4_gemm_parts(...) > 1 or M * top_k small against E, at most 4096
  * routed slots) sorted_token_ids and expert_offsets may both be NULL: the

@@ -209,7 +209,8 @@ def test_int4_gemm_stage_rejects_bad_arguments():
     assert g(dt=3) == _lib.XK_ERR_INVALID
     # flags: 0 is the only public value (the reference's bf16-rounded weights)
     assert g(flags=1) == _lib.XK_ERR_INVALID
-    assert _lib.query("xk_moe_int4_gemm_workspace_bytes", 4, 1024) == 0
+    # the prefill tile kernel's queue: one counter per XCD
+    assert _lib.query("xk_moe_int4_gemm_workspace_bytes", 4, 1024) == 32
 
 
 def test_combine_rejects_bad_arguments():

@@ -98,7 +98,7 @@ int launch_int4_rs(const void* A, bool f32a, int64_t M, int64_t K, const int32_t
 int launch_int4_prefill(const void* A, int64_t K, const int32_t* packed, const uint16_t* scale,
                         int64_t E, int64_t N, int64_t numel, int64_t top_k, int group_size,
                         const int32_t* sorted_ids, const int32_t* offsets, float* slot_out,
-                        hipStream_t stream);
+                        int* queue, hipStream_t stream);
 
 // Routed rows per expert (on average) from which the tile kernel replaces the
 // weight-streaming kernel, which streams every expert's weights once per
@@ -109,10 +109,13 @@ constexpr int64_t kPrefillRowsPerExpert = 17;
 
 // The INT4 kernels need no workspace; the argument and this size stay in the
 // interface (0 bytes, NULL accepted).
+int64_t int4_prefill_queue_bytes();
+
+// The tile kernel's queue; the other kernels need none.
 int64_t int4_gemm_workspace_bytes(int64_t M, int64_t K) {
   (void)M;
   (void)K;
-  return 0;
+  return int4_prefill_queue_bytes();
 }
 
 // The grouped-GEMM kernel a call runs, from its shapes and flags only (not
@@ -175,8 +178,6 @@ int launch_int4_gemm(const void* A, int a_dtype, int64_t M, int64_t K, const int
                      int num_global, const int32_t* sorted_ids, const int32_t* offsets,
                      float* slot_out, int flags, int64_t ep_global, void* workspace,
                      int64_t workspace_bytes, hipStream_t stream) {
-  (void)workspace;
-  (void)workspace_bytes;
   XK_REQUIRE(a_dtype == XK_DT_BF16 || a_dtype == XK_DT_FP32, "int4: bad A dtype %d", a_dtype);
   XK_REQUIRE((flags & ~(XK_INT4_TEST_FORCE_TILE | XK_INT4_TEST_FORCE_STREAM)) == 0,
              "int4: unknown flags 0x%x (pass 0)", flags);
@@ -202,8 +203,15 @@ int launch_int4_gemm(const void* A, int a_dtype, int64_t M, int64_t K, const int
   }
   switch (kern) {
     case Int4Kernel::kTile:
-      return launch_int4_prefill(A, K, packed, scale, E, N, numel, top_k, group_size, sorted_ids,
-                                 offsets, slot_out, stream);
+      // the tile queue lives in the workspace; without one the tiles are
+      // dealt statically
+      return launch_int4_prefill(
+          A, K, packed, scale, E, N, numel, top_k, group_size, sorted_ids, offsets, slot_out,
+          workspace != nullptr && workspace_bytes >= int4_prefill_queue_bytes() &&
+                  reinterpret_cast<uintptr_t>(workspace) % 4 == 0
+              ? static_cast<int*>(workspace)
+              : nullptr,
+          stream);
     case Int4Kernel::kRs:
       return launch_int4_rs(A, a_dtype == XK_DT_FP32, M, K, packed, scale, E, N, numel, top_k,
                             group_size, sorted_ids, offsets, topk_ids, emap, num_global, slot_out,

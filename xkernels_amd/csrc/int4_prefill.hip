@@ -63,6 +63,7 @@ struct PrefillArgs {
   float* out;              // [numel, N]
   int K, N, numel, top_k, num_experts;
   int glog;                // log2(group size / 32)
+  int* queue;              // [kXcds] tiles taken from each XCD's range (zero at launch), or null
 };
 
 // GBIG: groups of 64 or 128 (chunk 4 s + q's scale is scale[(4 s + q) >> glog]);
@@ -74,6 +75,7 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& p) {
   __shared__ int tok_lds[kPBM];
   __shared__ int slot_lds[kPBM];
   __shared__ int mt_prefix[kPMaxExperts + 1];
+  __shared__ int tile_lds;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int c16 = lane & 15, q = lane >> 4;
@@ -114,7 +116,36 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& p) {
   const int st_kv = tid & 15, st_g = tid >> 4;
   const int st_row = (st_g & 1) * 8 + ((st_g >> 1) & 7) + 16 * (st_g >> 4);
 
-  for (int t = t_beg + idx; t < t_end; t += per_xcd) {
+  // Tile order. With a queue, each workgroup takes the next tile of its
+  // XCD's range (an atomic per tile, by one thread) and, when that range is
+  // exhausted, the next tiles of the other XCDs' ranges: workgroups that
+  // finish early (ranges of half tiles, a faster CU) take over the rest, and
+  // every workgroup exits once all ranges are taken. Without one, workgroup
+  // idx of an XCD takes tiles idx, idx + per_xcd, ... of its range.
+  int t_next = t_beg + idx;
+  for (;;) {
+    __syncthreads();  // the previous tile is done with tile_lds, slot_lds and a_lds
+    if (tid == 0) {
+      int tt = -1;
+      if (p.queue == nullptr) {
+        tt = t_next < t_end ? t_next : -1;
+        t_next += per_xcd;
+      } else {
+        for (int k = 0; k < kXcds && tt < 0; ++k) {
+          const int x = (xcd + k) % kXcds;
+          const int b0 = static_cast<int>(static_cast<int64_t>(T) * x / kXcds);
+          const int b1 = static_cast<int>(static_cast<int64_t>(T) * (x + 1) / kXcds);
+          if (b0 < b1) {
+            const int n = atomicAdd(&p.queue[x], 1);
+            if (b0 + n < b1) tt = b0 + n;
+          }
+        }
+      }
+      tile_lds = tt;
+    }
+    __syncthreads();
+    const int t = tile_lds;
+    if (t < 0) break;
     const int mtile = t / NB, nb = t - mtile * NB;
     int lo = 0, hi = E;  // mt_prefix[lo] <= mtile < mt_prefix[hi]
     while (hi - lo > 1) {
@@ -126,7 +157,6 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& p) {
     const int rows = min(kPBM, p.offsets[e + 1] - row0);
     const int n0 = nb * kPBN + wn * (kCT * 16);
 
-    __syncthreads();  // the previous tile is done with slot_lds / a_lds
     if (tid < kPBM) {
       int slot = -1, tok = -1;
       if (tid < rows) {
@@ -264,6 +294,12 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& p) {
   }
 }
 
+// Zeroes the tile queue before the tile kernel (a kernel, not a memset, so
+// that a captured graph holds no memset node).
+__global__ void clear_queue(int* q) {
+  if (threadIdx.x < kXcds) q[threadIdx.x] = 0;
+}
+
 __global__ void __launch_bounds__(kPThreads)
 int4_prefill_gemm(PrefillArgs p) {
   prefill_body<false>(p);
@@ -278,6 +314,9 @@ int4_prefill_gemm_g(PrefillArgs p) {
 
 int device_cu_count();
 
+// Bytes of the tile kernel's queue (its workspace).
+int64_t int4_prefill_queue_bytes() { return kXcds * sizeof(int); }
+
 // Shapes the tile kernel takes: bf16 activations, group 32, K a multiple of two
 // steps, N a multiple of the column tile, at most kPMaxExperts local experts.
 bool int4_prefill_ok(int a_dtype, int group_size, int64_t K, int64_t N, int64_t E) {
@@ -288,12 +327,16 @@ bool int4_prefill_ok(int a_dtype, int group_size, int64_t K, int64_t N, int64_t 
 int launch_int4_prefill(const void* A, int64_t K, const int32_t* packed, const uint16_t* scale,
                         int64_t E, int64_t N, int64_t numel, int64_t top_k, int group_size,
                         const int32_t* sorted_ids, const int32_t* offsets, float* slot_out,
-                        hipStream_t stream) {
+                        int* queue, hipStream_t stream) {
   XK_REQUIRE(reinterpret_cast<uintptr_t>(A) % 16 == 0 && reinterpret_cast<uintptr_t>(packed) % 16 == 0,
              "int4 prefill: A and packed must be 16-byte aligned");
+  if (queue != nullptr) {
+    hipLaunchKernelGGL(clear_queue, dim3(1), dim3(64), 0, stream, queue);
+    XK_CHECK_LAUNCH("clear_queue");
+  }
   PrefillArgs a{static_cast<const uint16_t*>(A), reinterpret_cast<const uint32_t*>(packed), scale,
                 sorted_ids, offsets, slot_out, int(K), int(N), int(numel), int(top_k), int(E),
-                group_size == 128 ? 2 : group_size == 64 ? 1 : 0};
+                group_size == 128 ? 2 : group_size == 64 ? 1 : 0, queue};
   // one workgroup per CU, a multiple of the XCD count
   const int cus = device_cu_count();
   const int grid = std::max(kXcds, cus / kXcds * kXcds);
