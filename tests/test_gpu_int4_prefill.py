@@ -37,8 +37,10 @@ def _fused(A, packed, scale, ids, w, flags, emap=None, mul=1):
     return out
 
 
-def _slot_rows(A, packed, scale, ids, flags):
-    """Align (block 16) then the GEMM stage alone: fp32 rows per routed slot."""
+def _slot_rows(A, packed, scale, ids, flags, gws=None):
+    """Align (block 16) then the GEMM stage alone: fp32 rows per routed slot
+    (gws: the GEMM's workspace, which holds the tile kernel's queue; without
+    one the tiles are dealt statically)."""
     M, K = A.shape
     E, N, _ = packed.shape
     k = ids.shape[1]
@@ -59,7 +61,8 @@ def _slot_rows(A, packed, scale, ids, flags):
     slot_out = torch.full((parts, numel, N), float("nan"), dtype=torch.float32, device=dev)
     _lib.call("xk_moe_int4_w4a16_gemm", A.data_ptr(), _lib.XK_DT_BF16, M, K, packed.data_ptr(),
               scale.data_ptr(), E, N, 32, ids.data_ptr(), k, None, 0, sorted_ids.data_ptr(),
-              offsets.data_ptr(), slot_out.data_ptr(), flags, None, 0, _stream())
+              offsets.data_ptr(), slot_out.data_ptr(), flags, None if gws is None else gws.data_ptr(),
+              0 if gws is None else gws.numel(), _stream())
     return slot_out.sum(0)
 
 
@@ -90,6 +93,25 @@ def test_tile_kernel_rows_match_stream_kernel(M, E, N, K, top_k, routing, dev):
     torch.cuda.synchronize()
     assert not torch.isnan(tile).any(), "a routed slot row was not written"
     assert_close(tile, stream, 1e-4, 1e-4 * float(stream.abs().mean()), "tile vs stream rows")
+
+
+@pytest.mark.parametrize("M,E,N,K,top_k,routing", CASES)
+def test_tile_queue_equals_static_deal(M, E, N, K, top_k, routing, dev):
+    """The tile queue (workgroups take tiles atomically, then the other XCDs'
+    ranges) computes every tile exactly once: its rows equal the static deal's
+    bit for bit, from a buffer of NaNs, over two calls with one workspace."""
+    print(f"tile queue M={M} E={E} N={N} K={K} k={top_k} {routing}", flush=True)
+    ids = zipf_topk(M, top_k, E, 1.2, M + 7) if routing == "zipf" else uniform_topk(M, top_k, E, M + 7)
+    A, packed, scale, ids, _ = _inputs(M, E, N, K, ids, seed=M + 9)
+    need = _lib.query("xk_moe_int4_gemm_workspace_bytes", M, K)
+    assert need > 0
+    gws = torch.randint(0, 256, (need,), dtype=torch.uint8, device=dev)  # the queue is cleared per call
+    static = _slot_rows(A, packed, scale, ids, _lib._XK_INT4_TEST_FORCE_TILE)
+    for _ in range(2):
+        queued = _slot_rows(A, packed, scale, ids, _lib._XK_INT4_TEST_FORCE_TILE, gws)
+        torch.cuda.synchronize()
+        assert not torch.isnan(queued).any(), "a routed slot row was not written"
+        assert torch.equal(queued, static)
 
 
 @pytest.mark.parametrize("M,E,N,K,top_k,routing", CASES)
