@@ -264,14 +264,38 @@ __device__ __forceinline__ void stream_body(const RsArgs& p) {
   const int gsz = paired ? static_cast<int>(gridDim.x) / S : static_cast<int>(gridDim.x);
   const int grp = paired ? (b / (8 * S)) * 8 + (b & 7) : b;
   const int s_fixed = paired ? (b >> 3) % S : 0;
-  const int64_t seg_cost = ncp + kRsSegGap<FMT>;
+  const int seg_cost = ncp + kRsSegGap<FMT>;
   const int64_t cost_total = static_cast<int64_t>(total_items / ncp) * seg_cost;
   auto item_at = [&](int64_t v) {  // first real item at or after cost v
     const int64_t sg = v / seg_cost, off = v - sg * seg_cost;
     return static_cast<int>(sg * ncp + (off > kRsSegGap<FMT> ? off - kRsSegGap<FMT> : 0));
   };
-  const int item_beg = item_at(cost_total * grp / gsz);
-  const int item_end = item_at(cost_total * (grp + 1) / gsz);
+  int item_beg, item_end;
+  if (cost_total < (int64_t(1) << 30)) {
+    // 32-bit divisions (the 64-bit ones cost ~0.5 us at the workgroup's start):
+    // with cost_total = cq gsz + cr, cost_total g / gsz = cq g + cr g / gsz
+    const int ct = static_cast<int>(cost_total), cq = ct / gsz, cr = ct - cq * gsz;
+    auto item_at32 = [&](int v) {
+      const int sg = v / seg_cost, off = v - sg * seg_cost;
+      return sg * ncp + (off > kRsSegGap<FMT> ? off - kRsSegGap<FMT> : 0);
+    };
+    item_beg = item_at32(cq * grp + cr * grp / gsz);
+    item_end = item_at32(cq * (grp + 1) + cr * (grp + 1) / gsz);
+  } else {
+    item_beg = item_at(cost_total * grp / gsz);
+    item_end = item_at(cost_total * (grp + 1) / gsz);
+  }
+  // The expert whose items hold position pos: the largest e with pref[e] <= pos
+  // (experts without items share their prefix with the next one), counted by
+  // one ballot per 64 experts.
+  auto expert_of = [&](int pos) __attribute__((always_inline)) {
+    int n = 0;
+    for (int base = 1; base < E; base += 64) {
+      const int e = base + lane;
+      n += __popcll(__ballot(e < E && pref[e] <= pos));
+    }
+    return uniform(n);
+  };
 
   const int w_lane = c16 * KW * 4 + q * 16;  // bytes; + 64 h: group 4 h + q of the line
   const int s_lane = c16 * G * SB;           // bytes: start of column c16's scale row
@@ -290,12 +314,7 @@ __device__ __forceinline__ void stream_body(const RsArgs& p) {
   if constexpr (FMT == kFmtInt4) {
     int rot2 = 0, pos2 = item_beg;
     while (pos2 < item_end) {
-      int lo = 0, hi = E;
-      while (hi - lo > 1) {
-        const int mid = (lo + hi) >> 1;
-        if (pref[mid] <= pos2) lo = mid; else hi = mid;
-      }
-      const int e = uniform(lo);
+      const int e = expert_of(pos2);
       const int local = pos2 - pref[e];
       const int cp0 = local % ncp;
       const int cpe = min(ncp, cp0 + (item_end - pos2));
@@ -669,12 +688,7 @@ __device__ __forceinline__ void stream_body(const RsArgs& p) {
   int rot = 0;      // first wave to take a remainder pair in the next chunk
   int pos = item_beg;
   while (pos < item_end) {
-    int lo = 0, hi = E;  // largest e with pref[e] <= pos
-    while (hi - lo > 1) {
-      const int mid = (lo + hi) >> 1;
-      if (pref[mid] <= pos) lo = mid; else hi = mid;
-    }
-    const int e = uniform(lo);
+    const int e = expert_of(pos);
     const int local = pos - pref[e];
     const int seg = local / ncp, cp0 = local - seg * ncp;  // seg = pass (* S + slice)
     const int pass = paired ? seg : seg / S, s = paired ? s_fixed : seg - pass * S;
