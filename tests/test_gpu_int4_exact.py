@@ -338,3 +338,62 @@ def test_random_shapes_within_bound(case):
                        emap=emap)
     else:
         _bounded_check(A, packed, scale, ids, torch.nan_to_num(rows), emap=emap)
+
+
+def _sweep_cases_groups(n=16, seed=2027):
+    """Seeded random shapes over the eligibility added for groups of 64 and
+    128: K a multiple of 32 and of the group (odd scale counts per row load 2
+    bytes at a time), N a multiple of 16 (a half column pair), groups of 32, 64
+    or 128, some shapes large enough for the prefill tile kernel (N and K
+    multiples of 256), bf16 and fp32 activations, align-fed or self-routed,
+    with or without an expert map."""
+    import random
+    rng = random.Random(seed)
+    cases = []
+    for i in range(n):
+        E = rng.choice([2, 5, 8, 16, 33, 48])
+        gs = rng.choice([32, 64, 128])
+        N = 256 * rng.randint(1, 3) if rng.random() < 0.35 else 16 * rng.randint(1, 40)
+        K = 256 * rng.randint(1, 12) if rng.random() < 0.35 else gs * rng.randint(1, 4096 // gs)
+        cases.append(dict(M=rng.choice([1, 3, 16, 40, 64, 200, 600]), E=E, N=N, K=K,
+                          top_k=rng.randint(1, min(8, E)), gs=gs,
+                          routing=rng.choice(["uniform", "zipf"]), fp32=rng.random() < 0.25,
+                          self_route=rng.random() < 0.5, ep=rng.random() < 0.25, seed=300 + i))
+    return cases
+
+
+@pytest.mark.parametrize("case", _sweep_cases_groups(),
+                         ids=lambda c: "M{M}-E{E}-N{N}-K{K}-k{top_k}-g{gs}".format(**c))
+def test_random_group_shapes_within_bound(case):
+    c = case
+    M, E, N, K, top_k, gs = c["M"], c["E"], c["N"], c["K"], c["top_k"], c["gs"]
+    dt = _lib.XK_DT_FP32 if c["fp32"] else _lib.XK_DT_BF16
+    kern = _lib.query("xk_moe_int4_kernel", M, top_k, E, N, K, dt, gs, 0, 0)
+    print(f"group sweep {c} kernel {kern}", flush=True)
+    ids = (uniform_topk(M, top_k, E, c["seed"]) if c["routing"] == "uniform"
+           else zipf_topk(M, top_k, E, 1.2, c["seed"]))
+    A, packed, scale, ids = _device_inputs(M, E, N, K, ids, c["seed"], gs)
+    if c["fp32"]:
+        A = torch.randn(M, K, generator=torch.Generator(device="cuda").manual_seed(c["seed"]), device="cuda")
+    emap = None
+    if c["ep"] and E >= 2:
+        E_loc = E // 2
+        emap = torch.full((E,), -1, dtype=torch.int32, device="cuda")
+        emap[E - E_loc:] = torch.arange(E_loc, dtype=torch.int32, device="cuda")
+        packed, scale = packed[E - E_loc:].contiguous(), scale[E - E_loc:].contiguous()
+    rows = None
+    if c["self_route"]:
+        try:
+            rows = _gemm_rows(A, packed, scale, ids, emap=emap, self_route=True, gs=gs)
+        except RuntimeError as err:
+            assert "align outputs" in str(err), err
+    if rows is None:
+        rows = _gemm_rows(A, packed, scale, ids, emap=emap, gs=gs)
+    flat = ids.reshape(-1).long()
+    local = torch.ones_like(flat, dtype=torch.bool) if emap is None else emap.long()[flat] >= 0
+    assert not torch.isnan(rows[local]).any(), "a routed local slot's row was not written"
+    if c["fp32"]:
+        _bounded_check(A, packed, scale, ids, torch.nan_to_num(rows), rel=REL_F32, w_dtype=torch.float32,
+                       emap=emap, gs=gs)
+    else:
+        _bounded_check(A, packed, scale, ids, torch.nan_to_num(rows), emap=emap, gs=gs)
