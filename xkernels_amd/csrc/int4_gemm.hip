@@ -85,7 +85,7 @@ bool int4_use_stream(int a_dtype, int group_size, int64_t K) {
          int4_rs_group_ok(K, group_size);
 }
 
-bool int4_prefill_ok(int a_dtype, int group_size, int64_t K, int64_t N, int64_t E);
+bool int4_prefill_ok(int a_dtype, int group_size, int64_t M, int64_t K, int64_t N, int64_t E);
 bool int4_rs_ok(int64_t M, int64_t top_k, int64_t K, int64_t N, int64_t E, bool f32a,
                 int group_size);
 int int4_rs_slices(int64_t K, int64_t N, int64_t numel, int64_t E, bool f32a);
@@ -134,7 +134,7 @@ Int4Kernel int4_choose(int64_t M, int64_t top_k, int64_t E, int64_t N, int64_t K
   const int64_t numel = M * top_k;
   const int64_t local = ep_global > E ? (numel * E + ep_global - 1) / ep_global : numel;
   const bool f32a = a_dtype == XK_DT_FP32;
-  const bool tile_ok = !f32a && int4_prefill_ok(a_dtype, group_size, K, N, E);
+  const bool tile_ok = !f32a && int4_prefill_ok(a_dtype, group_size, M, K, N, E);
   const bool rs_ok = int4_rs_ok(M, top_k, K, N, E, f32a, group_size);
   bool tile = tile_ok && local >= kPrefillRowsPerExpert * E;
   if (flags & XK_INT4_TEST_FORCE_TILE) tile = tile_ok;

@@ -9,7 +9,7 @@
 //
 // With hundreds of routed rows per expert the work is contraction bound, so the
 // kernel is an MFMA tile GEMM:
-//   * a tile is (expert e, 128 consecutive rows of e's padded slot range, 256
+//   * a tile is (expert e, 256 consecutive rows of e's padded slot range, 256
 //     output columns); tiles are enumerated on the device from the align
 //     offsets, so no host synchronisation is needed;
 //   * a persistent grid (one workgroup per CU) walks the tiles; tiles are cut
@@ -17,11 +17,14 @@
 //     the column blocks of one row block are adjacent in a range, so the
 //     workgroups running together on an XCD share the row block's activations
 //     in that XCD's L2;
-//   * 8 waves split the 256 columns; each wave owns all 128 rows x 32 columns
-//     (8 x 2 tiles of v_mfma_f32_16x16x32_bf16, 64 accumulator registers), so
-//     every weight is dequantised by exactly one wave;
-//   * per 128-k step the 128 gathered activation rows are staged in LDS (double
-//     buffered) as they are (the dequant emits natural k order). gfx950 serves a 16-byte LDS read for 32 lanes at a time from 128
+//   * 8 waves split the 256 columns; each wave owns all 256 rows x 32 columns
+//     (16 x 2 tiles of v_mfma_f32_16x16x32_bf16, 128 accumulator registers), so
+//     every weight is dequantised by exactly one wave, once per 256 rows. On
+//     gfx950 the dequant's VALU work does not overlap the MFMAs of its SIMD, so
+//     the rows a dequantised weight serves set the kernel's speed;
+//   * per 128-k step the 256 gathered activation rows are staged in LDS (double
+//     buffered, one staging register set loaded a step ahead and written after
+//     the step's MFMAs) as they are (the dequant emits natural k order). gfx950 serves a 16-byte LDS read for 32 lanes at a time from 128
 //     banks, so the 32 lanes (16 rows x 2 lane groups) of one read must hit 32
 //     distinct 16-byte bank groups: rows are 288 bytes apart (18 groups) and the
 //     16-byte chunk (lane group q, MFMA j) of a row sits at chunk 4j + q, which
@@ -39,7 +42,7 @@
 namespace xk {
 namespace {
 
-constexpr int kPBM = 128;              // routed rows per tile
+constexpr int kPBM = 256;              // routed rows per tile
 constexpr int kPBN = 256;              // output columns per tile
 constexpr int kPBK = 128;              // k per pipeline step (4 quantisation groups)
 constexpr int kWM = 1;                 // waves along the rows
@@ -64,6 +67,7 @@ struct PrefillArgs {
   int K, N, numel, top_k, num_experts;
   int glog;                // log2(group size / 32)
   int* queue;              // [kXcds] tiles taken from each XCD's range (zero at launch), or null
+  int a_bytes;             // bytes of A
 };
 
 // GBIG: groups of 64 or 128 (chunk 4 s + q's scale is scale[(4 s + q) >> glog]);
@@ -168,32 +172,41 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& p) {
     }
     __syncthreads();
 
-    // Tiles of at most 64 rows (an expert's last row block) run half the MFMAs
-    // and half the activation staging (C5: 2,191-2,204 -> 2,175-2,185 us).
+    // An expert's last row block of at most 128 or 64 rows runs a half- or
+    // quarter-height tile: fewer MFMAs and staging passes, the same dequant.
     auto run_tile = [&](auto rt_c) __attribute__((always_inline)) {
     constexpr int RT = decltype(rt_c)::value;  // 16-row MFMA tiles
     constexpr int kSP = RT * 16 / kStRows;     // staging passes per step
     // Rows without a token read token 0: MFMA rows are independent and those
     // rows are never stored, so every load stays unconditional.
-    const u32x4* a_src[kSP];
+    // Loads go through buffer resources: a per-lane byte offset fixed for the
+    // tile and the step's offset in a scalar register (A below 2^31 bytes and
+    // one expert's weights below 2^31 bytes, checked by int4_prefill_ok).
+    const __amdgpu_buffer_rsrc_t ra =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(p.A), 0, p.a_bytes, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint32_t*>(p.packed + static_cast<int64_t>(e) * N * KW), 0, N * KW * 4, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(p.scale + static_cast<int64_t>(e) * N * G), 0, N * G * 2, 0x00020000);
+    uint32_t a_off[kSP];
 #pragma unroll
     for (int i = 0; i < kSP; ++i) {
       const int tok = max(tok_lds[st_row + kStRows * i], 0);
-      a_src[i] = reinterpret_cast<const u32x4*>(p.A + static_cast<int64_t>(tok) * K) + st_kv;
+      a_off[i] = (static_cast<uint32_t>(tok) * static_cast<uint32_t>(K) + st_kv * 8) * 2;
     }
-    const u32x4* wrow[kCT];
-    const uint16_t* srow[kCT];
+    uint32_t w_off[kCT], s_off[kCT];
 #pragma unroll
     for (int c = 0; c < kCT; ++c) {
-      const int64_t n = static_cast<int64_t>(e) * N + n0 + 16 * c + c16;
-      wrow[c] = reinterpret_cast<const u32x4*>(p.packed + n * KW) + q;
-      srow[c] = p.scale + n * G;
+      const uint32_t n = n0 + 16 * c + c16;
+      w_off[c] = (n * KW + q * 4) * 4;
+      s_off[c] = (n * G + (q >> glog)) * 2;
     }
 
     auto load_a = [&](int s, u32x4 (&ar)[kSP]) {
       s = min(s, steps - 1);
 #pragma unroll
-      for (int i = 0; i < kSP; ++i) ar[i] = a_src[i][s * (kPBK / 8)];
+      for (int i = 0; i < kSP; ++i)
+        ar[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(ra, a_off[i], s * (kPBK * 2), 0));
     };
     auto store_a = [&](int buf, const u32x4 (&ar)[kSP]) {
 #pragma unroll
@@ -208,8 +221,9 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& p) {
       s = min(s, steps - 1);
 #pragma unroll
       for (int c = 0; c < kCT; ++c) {
-        w[c] = wrow[c][s * (kPBK / 32)];
-        sv[c] = srow[c][(s * (kPBK / 32) + q) >> glog];  // chunk 4 s + q's group
+        w[c] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, w_off[c], s * (kPBK / 2), 0));
+        // chunk 4 s + q's group: (4 s + q) >> glog = s (4 >> glog) + (q >> glog)
+        sv[c] = __builtin_amdgcn_raw_buffer_load_b16(rs, s_off[c], s * ((kPBK / 32) >> glog) * 2, 0);
       }
     };
 
@@ -225,33 +239,50 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& p) {
       for (int c = 0; c < kCT; ++c) ks[c] = rne_scale(__uint_as_float(sv[c] << 16));
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        bf16x8 af[RT];
+        bf16x8 b[kCT];
 #pragma unroll
-        for (int i = 0; i < RT; ++i)
-          af[i] = *reinterpret_cast<const bf16x8*>(
+        for (int c = 0; c < kCT; ++c) b[c] = dequant_rne_nat(w[c][j], ks[c], kNibMask, kNibMaskHi);
+        // row tiles in groups of kAG: the next group's operands are read while
+        // the current group's MFMAs run (bounds the registers in flight)
+        constexpr int kAG = RT < 2 ? RT : 2;
+        auto rd = [&](int i) {
+          return *reinterpret_cast<const bf16x8*>(
               &a_lds[buf][(wm * RT * 16 + i * 16 + c16) * kPStride + (j * 4 + q) * 8]);
+        };
+        bf16x8 af[kAG];
 #pragma unroll
-        for (int c = 0; c < kCT; ++c) {
-          const bf16x8 b = dequant_rne_nat(w[c][j], ks[c], kNibMask, kNibMaskHi);
+        for (int u = 0; u < kAG; ++u) af[u] = rd(u);
 #pragma unroll
-          for (int i = 0; i < RT; ++i)
-            acc[i][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], b, acc[i][c], 0, 0, 0);
+        for (int g = 0; g < RT / kAG; ++g) {
+          bf16x8 an[kAG];
+          if (g + 1 < RT / kAG) {
+#pragma unroll
+            for (int u = 0; u < kAG; ++u) an[u] = rd((g + 1) * kAG + u);
+          }
+          __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+          for (int u = 0; u < kAG; ++u)
+#pragma unroll
+            for (int c = 0; c < kCT; ++c)
+              acc[g * kAG + u][c] =
+                  __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[u], b[c], acc[g * kAG + u][c], 0, 0, 0);
+          __builtin_amdgcn_sched_barrier(0);
+          if (g + 1 < RT / kAG) {
+#pragma unroll
+            for (int u = 0; u < kAG; ++u) af[u] = an[u];
+          }
         }
       }
     };
 
-    u32x4 a0[kSP], a1[kSP], w0[kCT], w1[kCT];
+    u32x4 a0[kSP], w0[kCT], w1[kCT];
     uint32_t s0[kCT], s1[kCT];
-    // Prologue: A(0) staged, then the loads in the order the loop leaves them
-    // outstanding at its head (A(s+1), W(s), A(s+2), W(s+1)), so the load
-    // counter waits the compiler derives for both paths into the loop agree.
+    // Prologue: A(0) staged, then W(0) and W(1), the loads the loop expects
+    // outstanding at its head.
     load_a(0, a0);
     store_a(0, a0);
-    load_a(1, a1);
     __builtin_amdgcn_sched_barrier(0);
     load_w(0, w0, s0);
-    __builtin_amdgcn_sched_barrier(0);
-    load_a(2, a0);
     __builtin_amdgcn_sched_barrier(0);
     load_w(1, w1, s1);
     __builtin_amdgcn_sched_barrier(0);
@@ -262,18 +293,19 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& p) {
     // (scheduling barriers keep the compiler from sinking the activation loads
     // to their use or hoisting the next store's permutes into compute(), either
     // of which would make a step wait for loads issued in the same step)
-    auto step = [&](int s, u32x4 (&ar)[kSP], u32x4 (&w)[kCT], uint32_t (&sv)[kCT]) {
+    auto step = [&](int s, u32x4 (&w)[kCT], uint32_t (&sv)[kCT]) {
       __syncthreads();
-      store_a((s + 1) & 1, ar);
-      load_a(s + 3, ar);
+      load_a(s + 1, a0);
       __builtin_amdgcn_sched_barrier(0);
       compute(s & 1, w, sv);
       __builtin_amdgcn_sched_barrier(0);
       load_w(s + 2, w, sv);
+      __builtin_amdgcn_sched_barrier(0);
+      store_a((s + 1) & 1, a0);
     };
     for (int s = 0; s < steps; s += 2) {
-      step(s, a1, w0, s0);
-      step(s + 1, a0, w1, s1);
+      step(s, w0, s0);
+      step(s + 1, w1, s1);
     }
 
 #pragma unroll
@@ -287,7 +319,9 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& p) {
         for (int c = 0; c < kCT; ++c) orow[16 * c] = acc[i][c][v];
       }
     };
-    if (rows <= kPBM / 2)
+    if (rows <= kPBM / 4)
+      run_tile(std::integral_constant<int, kRT / 4>{});
+    else if (rows <= kPBM / 2)
       run_tile(std::integral_constant<int, kRT / 2>{});
     else
       run_tile(std::integral_constant<int, kRT>{});
@@ -317,11 +351,14 @@ int device_cu_count();
 // Bytes of the tile kernel's queue (its workspace).
 int64_t int4_prefill_queue_bytes() { return kXcds * sizeof(int); }
 
-// Shapes the tile kernel takes: bf16 activations, group 32, K a multiple of two
-// steps, N a multiple of the column tile, at most kPMaxExperts local experts.
-bool int4_prefill_ok(int a_dtype, int group_size, int64_t K, int64_t N, int64_t E) {
+// Shapes the tile kernel takes: bf16 activations, groups of 32, 64 or 128, K a
+// multiple of two steps, N a multiple of the column tile, at most kPMaxExperts
+// local experts, A and one expert's packed weights each below 2^31 bytes (the
+// reach of a buffer resource's 32-bit offsets).
+bool int4_prefill_ok(int a_dtype, int group_size, int64_t M, int64_t K, int64_t N, int64_t E) {
   return a_dtype == XK_DT_BF16 && (group_size == 32 || group_size == 64 || group_size == 128) &&
-         K % (2 * kPBK) == 0 && N % kPBN == 0 && E <= kPMaxExperts;
+         K % (2 * kPBK) == 0 && N % kPBN == 0 && E <= kPMaxExperts &&
+         M * K * 2 < (int64_t(1) << 31) && N * K / 2 < (int64_t(1) << 31);
 }
 
 int launch_int4_prefill(const void* A, int64_t K, const int32_t* packed, const uint16_t* scale,
@@ -330,13 +367,16 @@ int launch_int4_prefill(const void* A, int64_t K, const int32_t* packed, const u
                         int* queue, hipStream_t stream) {
   XK_REQUIRE(reinterpret_cast<uintptr_t>(A) % 16 == 0 && reinterpret_cast<uintptr_t>(packed) % 16 == 0,
              "int4 prefill: A and packed must be 16-byte aligned");
+  const int64_t a_bytes = numel / std::max<int64_t>(top_k, 1) * K * 2;
+  XK_REQUIRE(a_bytes < (int64_t(1) << 31) && N * K / 2 < (int64_t(1) << 31),
+             "int4 prefill: A and one expert's weights must each be below 2^31 bytes");
   if (queue != nullptr) {
     hipLaunchKernelGGL(clear_queue, dim3(1), dim3(64), 0, stream, queue);
     XK_CHECK_LAUNCH("clear_queue");
   }
   PrefillArgs a{static_cast<const uint16_t*>(A), reinterpret_cast<const uint32_t*>(packed), scale,
                 sorted_ids, offsets, slot_out, int(K), int(N), int(numel), int(top_k), int(E),
-                group_size == 128 ? 2 : group_size == 64 ? 1 : 0, queue};
+                group_size == 128 ? 2 : group_size == 64 ? 1 : 0, queue, int(a_bytes)};
   // one workgroup per CU, a multiple of the XCD count
   const int cus = device_cu_count();
   const int grid = std::max(kXcds, cus / kXcds * kXcds);
