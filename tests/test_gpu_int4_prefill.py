@@ -1,11 +1,13 @@
-"""The prefill-regime INT4 tile kernel (MFMA tiles of 128 routed rows x 256
+"""The prefill-regime INT4 tile kernel (MFMA tiles of 256 routed rows x 256
 columns) against the oracle and against the decode stream kernel.
 
 Both kernels dequantise to the reference's bf16-rounded weights, so their fp32
 per-slot rows differ only by fp32 summation order (checked at 1e-4 relative);
 the fused outputs meet the op spec's bf16 tolerance against the oracle. Cases
 cover skewed (Zipf) routing with partial and empty row blocks, experts with no
-tokens, more tiles than workgroups, expert parallelism and the unweighted sum.
+tokens, more tiles than workgroups, expert parallelism and the unweighted sum,
+and fixed per-expert row counts that give every tile height (256, 192, 128 and
+64 rows) and every tile order class.
 """
 from __future__ import annotations
 
@@ -74,19 +76,39 @@ def _inputs(M, E, N, K, ids, seed, scale_hi=0.02):
     return A, packed, scale, ids.to(torch.int32).cuda(), w
 
 
+# Routed rows per expert for the "classes" routing (top_k = 1; the align pads
+# each expert to 16 rows): 608 = two full blocks + a 96-row tail, 176 and 144
+# (129-192-row tails), 256 (exactly one full block), 32, none, 240 (a tail above
+# 192 rows, ordered with the full blocks), 80 (65-128), 704 = two full blocks +
+# a 192-row tail.
+CLASS_ROWS = [600, 170, 250, 30, 0, 230, 129, 65, 700]
+
+
+def _ids(M, top_k, E, routing, seed):
+    if routing == "zipf":
+        return zipf_topk(M, top_k, E, 1.2, seed)
+    if routing == "classes":
+        assert top_k == 1 and E == len(CLASS_ROWS) and M == sum(CLASS_ROWS)
+        ids = torch.cat([torch.full((n,), e, dtype=torch.int32) for e, n in enumerate(CLASS_ROWS)])
+        g = torch.Generator().manual_seed(seed)
+        return ids[torch.randperm(M, generator=g)].reshape(M, 1)
+    return uniform_topk(M, top_k, E, seed)
+
+
 CASES = [  # M, E, N, K, top_k, routing
     (300, 8, 512, 512, 4, "zipf"),      # partial row blocks, skew
     (1024, 16, 256, 1024, 2, "zipf"),   # some experts empty
     (96, 6, 768, 256, 3, "uniform"),    # one step pair, 3 column blocks
     (2048, 48, 1024, 2048, 8, "zipf"),  # more tiles than workgroups
     (16, 8, 1024, 2048, 2, "uniform"),  # C1 shape, forced onto the tile kernel
+    (sum(CLASS_ROWS), len(CLASS_ROWS), 512, 512, 1, "classes"),  # every tile height and order class
 ]
 
 
 @pytest.mark.parametrize("M,E,N,K,top_k,routing", CASES)
 def test_tile_kernel_rows_match_stream_kernel(M, E, N, K, top_k, routing, dev):
     print(f"tile vs stream M={M} E={E} N={N} K={K} k={top_k} {routing}", flush=True)
-    ids = zipf_topk(M, top_k, E, 1.2, M) if routing == "zipf" else uniform_topk(M, top_k, E, M)
+    ids = _ids(M, top_k, E, routing, M)
     A, packed, scale, ids, _ = _inputs(M, E, N, K, ids, seed=M + 3)
     tile = _slot_rows(A, packed, scale, ids, _lib._XK_INT4_TEST_FORCE_TILE)
     stream = _slot_rows(A, packed, scale, ids, _lib._XK_INT4_TEST_FORCE_STREAM)
@@ -101,7 +123,7 @@ def test_tile_queue_equals_static_deal(M, E, N, K, top_k, routing, dev):
     ranges) computes every tile exactly once: its rows equal the static deal's
     bit for bit, from a buffer of NaNs, over two calls with one workspace."""
     print(f"tile queue M={M} E={E} N={N} K={K} k={top_k} {routing}", flush=True)
-    ids = zipf_topk(M, top_k, E, 1.2, M + 7) if routing == "zipf" else uniform_topk(M, top_k, E, M + 7)
+    ids = _ids(M, top_k, E, routing, M + 7)
     A, packed, scale, ids, _ = _inputs(M, E, N, K, ids, seed=M + 9)
     need = _lib.query("xk_moe_int4_gemm_workspace_bytes", M, K)
     assert need > 0
@@ -117,7 +139,7 @@ def test_tile_queue_equals_static_deal(M, E, N, K, top_k, routing, dev):
 @pytest.mark.parametrize("M,E,N,K,top_k,routing", CASES)
 def test_tile_kernel_matches_oracle(M, E, N, K, top_k, routing, dev):
     print(f"tile vs oracle M={M} E={E} N={N} K={K} k={top_k} {routing}", flush=True)
-    ids = zipf_topk(M, top_k, E, 1.2, M + 1) if routing == "zipf" else uniform_topk(M, top_k, E, M + 1)
+    ids = _ids(M, top_k, E, routing, M + 1)
     A, packed, scale, ids, w = _inputs(M, E, N, K, ids, seed=M + 5)
     got = _fused(A, packed, scale, ids, w, _lib._XK_INT4_TEST_FORCE_TILE)
     assert_close(got, moe_w4a16_ref(A, packed, scale, ids, w), 2e-2, 2e-2, "tile fused")

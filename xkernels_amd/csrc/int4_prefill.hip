@@ -12,11 +12,13 @@
 //   * a tile is (expert e, 256 consecutive rows of e's padded slot range, 256
 //     output columns); tiles are enumerated on the device from the align
 //     offsets, so no host synchronisation is needed;
-//   * a persistent grid (one workgroup per CU) walks the tiles; tiles are cut
-//     into 8 contiguous ranges, one per XCD (workgroup b runs on XCD b % 8), and
-//     the column blocks of one row block are adjacent in a range, so the
-//     workgroups running together on an XCD share the row block's activations
-//     in that XCD's L2;
+//   * a persistent grid (one workgroup per CU) walks the tiles. Row blocks are
+//     ordered by height class (full blocks and tails above 192 rows, then tails
+//     of 129-192, 65-128 and at most 64 rows) and dealt round-robin to the 8
+//     XCDs (workgroup b runs on XCD b % 8); a block's column tiles are adjacent
+//     in its XCD's sequence, so the workgroups running together on an XCD share
+//     the row block's activations in that XCD's L2, and every XCD runs its
+//     costliest tiles first and its cheapest last;
 //   * 8 waves split the 256 columns; each wave owns all 256 rows x 32 columns
 //     (16 x 2 tiles of v_mfma_f32_16x16x32_bf16, 128 accumulator registers), so
 //     every weight is dequantised by exactly one wave, once per 256 rows. On
@@ -78,7 +80,8 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& p) {
   __shared__ __attribute__((aligned(16))) uint16_t a_lds[2][kPBM * kPStride];
   __shared__ int tok_lds[kPBM];
   __shared__ int slot_lds[kPBM];
-  __shared__ int mt_prefix[kPMaxExperts + 1];
+  __shared__ int mt_prefix[kPMaxExperts + 1];          // class-0 row blocks per expert (prefix)
+  __shared__ uint16_t cl_prefix[3][kPMaxExperts + 1];  // experts with a class-1/2/3 tail (prefix)
   __shared__ int tile_lds;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -91,28 +94,46 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& p) {
   const int E = p.num_experts;
   const uint32_t kNibMask = in_vgpr(0x000F000Fu), kNibMaskHi = in_vgpr(0x00F000F0u);
 
-  // Row blocks per expert, as an inclusive prefix (wave 0, 64 experts a round).
+  // Row blocks in classes by height: 0 = full blocks and tails above 192 rows,
+  // 1 = tails of 129-192, 2 = 65-128, 3 = at most 64 rows. Blocks are ordered
+  // by class, then expert, and dealt round-robin to the XCDs (block b to XCD
+  // b % 8, its column blocks consecutive there), so every XCD's sequence runs
+  // from the costliest tiles to the cheapest.
   if (wave == 0) {
-    int run = 0;
+    int run[4] = {0, 0, 0, 0};
     for (int base = 0; base < E; base += 64) {
       const int e = base + lane;
-      int x = e < E ? (p.offsets[e + 1] - p.offsets[e] + kPBM - 1) / kPBM : 0;
+      const int rws = e < E ? p.offsets[e + 1] - p.offsets[e] : 0;
+      const int full = rws / kPBM, tail = rws - full * kPBM;
+      int x[4] = {full + (tail > kPBM * 3 / 4), tail > kPBM / 2 && tail <= kPBM * 3 / 4,
+                  tail > kPBM / 4 && tail <= kPBM / 2, tail > 0 && tail <= kPBM / 4};
 #pragma unroll
-      for (int d = 1; d < 64; d <<= 1) {
-        const int y = __shfl_up(x, d);
-        if (lane >= d) x += y;
+      for (int c = 0; c < 4; ++c) {
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+          const int y = __shfl_up(x[c], d);
+          if (lane >= d) x[c] += y;
+        }
+        if (e < E) {
+          if (c == 0) mt_prefix[e + 1] = run[0] + x[0];
+          else cl_prefix[c - 1][e + 1] = static_cast<uint16_t>(run[c] + x[c]);
+        }
+        run[c] += __shfl(x[c], 63);
       }
-      if (e < E) mt_prefix[e + 1] = run + x;
-      run += __shfl(x, 63);
     }
-    if (lane == 0) mt_prefix[0] = 0;
+    if (lane == 0) {
+      mt_prefix[0] = 0;
+      cl_prefix[0][0] = cl_prefix[1][0] = cl_prefix[2][0] = 0;
+    }
   }
   __syncthreads();
-  const int T = mt_prefix[E] * NB;
+  const int cb1 = mt_prefix[E], cb2 = cb1 + cl_prefix[0][E], cb3 = cb2 + cl_prefix[1][E];
+  const int B = cb3 + cl_prefix[2][E];
   const int xcd = blockIdx.x % kXcds, idx = blockIdx.x / kXcds;
   const int per_xcd = gridDim.x / kXcds;
-  const int t_beg = static_cast<int>(static_cast<int64_t>(T) * xcd / kXcds);
-  const int t_end = static_cast<int>(static_cast<int64_t>(T) * (xcd + 1) / kXcds);
+  // tiles of XCD x: its row blocks x, x + 8, ... times the column blocks
+  auto xcd_tiles = [&](int x) { return B > x ? (B - x + kXcds - 1) / kXcds * NB : 0; };
+  auto xcd_tile = [&](int x, int n) { return (x + kXcds * (n / NB)) * NB + n % NB; };
 
   // A staging: thread -> (row st_row + kStRows i, 16-byte chunk st_kv). The two
   // 16-lane halves of each 32-lane LDS write group take rows 8 apart, whose
@@ -120,28 +141,27 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& p) {
   const int st_kv = tid & 15, st_g = tid >> 4;
   const int st_row = (st_g & 1) * 8 + ((st_g >> 1) & 7) + 16 * (st_g >> 4);
 
-  // Tile order. With a queue, each workgroup takes the next tile of its
-  // XCD's range (an atomic per tile, by one thread) and, when that range is
-  // exhausted, the next tiles of the other XCDs' ranges: workgroups that
-  // finish early (ranges of half tiles, a faster CU) take over the rest, and
-  // every workgroup exits once all ranges are taken. Without one, workgroup
-  // idx of an XCD takes tiles idx, idx + per_xcd, ... of its range.
-  int t_next = t_beg + idx;
+  // Tile order. With a queue, each workgroup takes the next tile of its XCD's
+  // sequence (an atomic per tile, by one thread) and, when that sequence is
+  // exhausted, the next tiles of the other XCDs' sequences: workgroups that
+  // finish early take over the rest, and every workgroup exits once all
+  // sequences are taken. Without one, workgroup idx of an XCD takes tiles idx,
+  // idx + per_xcd, ... of its sequence.
+  int n_next = idx;
   for (;;) {
     __syncthreads();  // the previous tile is done with tile_lds, slot_lds and a_lds
     if (tid == 0) {
       int tt = -1;
       if (p.queue == nullptr) {
-        tt = t_next < t_end ? t_next : -1;
-        t_next += per_xcd;
+        tt = n_next < xcd_tiles(xcd) ? xcd_tile(xcd, n_next) : -1;
+        n_next += per_xcd;
       } else {
         for (int k = 0; k < kXcds && tt < 0; ++k) {
           const int x = (xcd + k) % kXcds;
-          const int b0 = static_cast<int>(static_cast<int64_t>(T) * x / kXcds);
-          const int b1 = static_cast<int>(static_cast<int64_t>(T) * (x + 1) / kXcds);
-          if (b0 < b1) {
+          const int nx = xcd_tiles(x);
+          if (nx > 0) {
             const int n = atomicAdd(&p.queue[x], 1);
-            if (b0 + n < b1) tt = b0 + n;
+            if (n < nx) tt = xcd_tile(x, n);
           }
         }
       }
@@ -150,14 +170,28 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& p) {
     __syncthreads();
     const int t = tile_lds;
     if (t < 0) break;
-    const int mtile = t / NB, nb = t - mtile * NB;
-    int lo = 0, hi = E;  // mt_prefix[lo] <= mtile < mt_prefix[hi]
-    while (hi - lo > 1) {
-      const int mid = (lo + hi) >> 1;
-      if (mt_prefix[mid] <= mtile) lo = mid; else hi = mid;
+    const int rb = t / NB, nb = t - rb * NB;
+    int e, row0;
+    if (rb < cb1) {
+      int lo = 0, hi = E;  // mt_prefix[lo] <= rb < mt_prefix[hi]
+      while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (mt_prefix[mid] <= rb) lo = mid; else hi = mid;
+      }
+      e = lo;
+      row0 = p.offsets[e] + (rb - mt_prefix[e]) * kPBM;
+    } else {
+      const int c = rb < cb2 ? 0 : rb < cb3 ? 1 : 2;
+      const int r = rb - (c == 0 ? cb1 : c == 1 ? cb2 : cb3);
+      const uint16_t* pre = cl_prefix[c];
+      int lo = 0, hi = E;  // pre[lo] <= r < pre[hi]
+      while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (pre[mid] <= r) lo = mid; else hi = mid;
+      }
+      e = lo;
+      row0 = p.offsets[e] + (p.offsets[e + 1] - p.offsets[e]) / kPBM * kPBM;
     }
-    const int e = lo;
-    const int row0 = p.offsets[e] + (mtile - mt_prefix[e]) * kPBM;
     const int rows = min(kPBM, p.offsets[e + 1] - row0);
     const int n0 = nb * kPBN + wn * (kCT * 16);
 
@@ -172,8 +206,8 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& p) {
     }
     __syncthreads();
 
-    // An expert's last row block of at most 128 or 64 rows runs a half- or
-    // quarter-height tile: fewer MFMAs and staging passes, the same dequant.
+    // An expert's last row block of at most 192, 128 or 64 rows runs a
+    // shorter tile: fewer MFMAs and staging passes, the same dequant.
     auto run_tile = [&](auto rt_c) __attribute__((always_inline)) {
     constexpr int RT = decltype(rt_c)::value;  // 16-row MFMA tiles
     constexpr int kSP = RT * 16 / kStRows;     // staging passes per step
@@ -323,6 +357,8 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& p) {
       run_tile(std::integral_constant<int, kRT / 4>{});
     else if (rows <= kPBM / 2)
       run_tile(std::integral_constant<int, kRT / 2>{});
+    else if (rows <= kPBM * 3 / 4)
+      run_tile(std::integral_constant<int, kRT * 3 / 4>{});
     else
       run_tile(std::integral_constant<int, kRT>{});
   }
