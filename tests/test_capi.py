@@ -189,6 +189,12 @@ def test_int4_kernel_choice_query():
     assert k(4096, 8, 48, 4096, 7168, bf, 32, _lib._XK_INT4_TEST_FORCE_STREAM) == 1
     assert k(512, 8, 48, 4096, 7168, bf, 32, 0, 0) == 2    # 85 rows per expert
     assert k(512, 8, 48, 4096, 7168, bf, 32, 0, 384) == 1  # 10.7 expected per local expert
+    # the MFMA kernels address A and one expert's weights through 32-bit buffer
+    # offsets: past 2^31 bytes the call falls back to the scalar kernel
+    assert k(149796, 8, 48, 4096, 7168, bf, 32) == 2     # A: 2^31 - 8,192 bytes
+    assert k(149797, 8, 48, 4096, 7168, bf, 32) == 0     # A: 2^31 + 6,144 bytes
+    assert k(256, 1, 1, 4096, 1048320, bf, 32) == 2      # one expert's weights just below 2^31 bytes
+    assert k(256, 1, 1, 4096, 1048576, bf, 32) == 0      # 2^31 bytes
 
 
 def test_int4_noalloc_rejects_unknown_flags():
