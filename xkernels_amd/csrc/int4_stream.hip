@@ -505,7 +505,8 @@ __device__ __forceinline__ void stream_body(const RsArgs& p) {
       // loads bytes 16 (q + 4 i) .. + 15 of the block's scales (lines pl +
       // (q + 4 i) L .. + L - 1, L = 16-byte loads per line; contiguous bytes
       // per column)
-      const bool blk = (pl & (kRsScLines - 1)) == 0 && pst < steps;
+      const bool blk = uniform(((pl & (kRsScLines - 1)) == 0 && pst < steps) ? 1 : 0) != 0;
+      const int lines_left = nl - pl;  // scalar: the per-lane test below is one compare
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
 #pragma unroll
@@ -517,7 +518,7 @@ __device__ __forceinline__ void stream_body(const RsArgs& p) {
           for (int i = 0; i < F::kScLoads; ++i)
           {
             const int lines = F::kLinesPerLoad << glog;  // lines one 16-byte piece covers
-            const bool in = (q + 4 * i) * lines < kRsScLines && pl + (q + 4 * i) * lines < nl;
+            const bool in = (q + 4 * i) * lines < kRsScLines && (q + 4 * i) * lines < lines_left;
             const int voff = in ? s_lane + 16 * (q + 4 * i) : (1 << 30);
             if constexpr (SLD == 2) {
 #pragma unroll
@@ -662,9 +663,9 @@ __device__ __forceinline__ void stream_body(const RsArgs& p) {
       const int cl1 = cl + (real ? 1 : 0);
       const bool tend = cl1 == nl;
       if (tend) finish_pair(ci);
-      cl = tend ? 0 : cl1;
-      ci += tend ? 1 : 0;
-      ++cst;
+      cl = uniform(tend ? 0 : cl1);
+      ci = uniform(ci + (tend ? 1 : 0));
+      cst = uniform(cst + 1);
       if constexpr (FMT == kFmtInt4) {
         // the wave with more steps left than its SIMD partner issues first
         left_lds[wave] = --left;
