@@ -629,16 +629,21 @@ __device__ __forceinline__ void stream_body(const RsArgs& p) {
       const uint32_t off =
           slot >= 0 ? static_cast<uint32_t>(((s * p.numel + slot) * N + (my_lo + i) * 32 + 4 * qa) * 4)
                     : kDrop;
-      static_for<kRsKeep>([&](auto I) {
-        if (nkeep == decltype(I)::value) {
-          keep[I][0] = acc[0];
-          keep[I][1] = acc[1];
-          keep_off[I] = off;
-          if constexpr (PADK)
-            keep_t1 = (keep_t1 & ~(1u << decltype(I)::value)) |
-                      (((my_lo + i) * 32 + 16 < N ? 1u : 0u) << decltype(I)::value);
-        }
-      });
+      // a uniform switch: only the kept slot's registers are written (an
+      // unrolled test of every slot compiles to selects over all of them)
+      switch (nkeep) {
+#define XK_KEEP(I)                                                                              \
+  case I:                                                                                       \
+    keep[I][0] = acc[0];                                                                        \
+    keep[I][1] = acc[1];                                                                        \
+    keep_off[I] = off;                                                                          \
+    if constexpr (PADK)                                                                         \
+      keep_t1 = (keep_t1 & ~(1u << I)) | (((my_lo + i) * 32 + 16 < N ? 1u : 0u) << I);          \
+    break;
+        XK_KEEP(0) XK_KEEP(1) XK_KEEP(2) XK_KEEP(3) XK_KEEP(4) XK_KEEP(5) XK_KEEP(6) XK_KEEP(7) XK_KEEP(8)
+#undef XK_KEEP
+        default: break;
+      }
       ++nkeep;
       acc[0] = acc[1] = f32x4{0.f, 0.f, 0.f, 0.f};
     };
