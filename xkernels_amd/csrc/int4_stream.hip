@@ -499,8 +499,14 @@ __device__ __forceinline__ void stream_body(const RsArgs& p) {
     Slot rg[kRsRing];
     auto issue = [&](Slot& sl) __attribute__((always_inline)) {
       const int cp = my_lo + pi;
-      const int wo = cp * 32 * KW * 4 + s * (Ks >> 1) + pl * 128;
-      const int so = cp * 32 * G * SB + ((s * (Ks >> 5) + pl * 8) >> glog) * SB;
+      // Scalar offsets. A load whose scalar offset the compiler cannot prove
+      // wave-uniform is wrapped in a loop over lane values: the MXFP4
+      // instantiation keeps its cursor in vector registers unless told (INT4
+      // keeps it scalar by itself, and there the extra read-first-lane costs
+      // vector instructions).
+      auto su = [](int x) { return FMT == kFmtInt4 ? x : uniform(x); };
+      const int wo = su(cp * 32 * KW * 4 + s * (Ks >> 1) + pl * 128);
+      const int so = su(cp * 32 * G * SB + ((s * (Ks >> 5) + pl * 8) >> glog) * SB);
       // scales: only on the first line of each block, where lane (c16, q)
       // loads bytes 16 (q + 4 i) .. + 15 of the block's scales (lines pl +
       // (q + 4 i) L .. + L - 1, L = 16-byte loads per line; contiguous bytes
@@ -543,9 +549,9 @@ __device__ __forceinline__ void stream_body(const RsArgs& p) {
       const int np = pst + 1;
       const int pl1 = pl + (np < steps ? 1 : 0);
       const bool lwrap = pl1 == nl;
-      pst = np;
-      pi += lwrap ? 1 : 0;
-      pl = lwrap ? 0 : pl1;
+      pst = su(np);
+      pi = su(pi + (lwrap ? 1 : 0));
+      pl = su(lwrap ? 0 : pl1);
     };
 
     f32x4 acc[2];  // the current column pair's two 16 x 16 tiles
