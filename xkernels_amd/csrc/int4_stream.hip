@@ -498,13 +498,13 @@ __device__ __forceinline__ void stream_body(const RsArgs& p) {
     };
     Slot rg[kRsRing];
     auto issue = [&](Slot& sl) __attribute__((always_inline)) {
-      const int cp = my_lo + pi;
       // Scalar offsets. A load whose scalar offset the compiler cannot prove
       // wave-uniform is wrapped in a loop over lane values: the MXFP4
       // instantiation keeps its cursor in vector registers unless told (INT4
       // keeps it scalar by itself, and there the extra read-first-lane costs
       // vector instructions).
       auto su = [](int x) { return FMT == kFmtInt4 ? x : uniform(x); };
+      const int cp = su(my_lo + pi);
       const int wo = su(cp * 32 * KW * 4 + s * (Ks >> 1) + pl * 128);
       const int so = su(cp * 32 * G * SB + ((s * (Ks >> 5) + pl * 8) >> glog) * SB);
       // scales: only on the first line of each block, where lane (c16, q)
