@@ -52,7 +52,6 @@ constexpr int kWN = 8;                 // waves along the columns
 constexpr int kPWaves = kWM * kWN;
 constexpr int kPThreads = kPWaves * 64;
 constexpr int kStRows = kPThreads / 16;    // activation rows staged per pass
-constexpr int kStPasses = kPBM / kStRows;  // staging passes per step
 constexpr int kRT = kPBM / kWM / 16;   // 16-row MFMA tiles per wave
 constexpr int kCT = kPBN / kWN / 16;   // 16-column MFMA tiles per wave
 constexpr int kPStride = kPBK + 16;    // bf16 per LDS row (72 dwords)
