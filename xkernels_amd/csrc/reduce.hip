@@ -208,11 +208,13 @@ int launch_reduce(const Tin* y, int64_t M, int top_k, int64_t H, const RowWeight
                   int64_t pstride = 0) {
   const bool aligned = (reinterpret_cast<uintptr_t>(y) % 16 == 0) &&
                        (reinterpret_cast<uintptr_t>(out) % 16 == 0) && (pstride % 8 == 0);
-  // fp32 inputs (the combine's per-slot rows) take 4 outputs per thread: a
-  // decode batch (M = 64, N = 4096) then spans every CU (measured 8.1 -> 6.2 us
-  // on the C2 combine); bf16 inputs keep one 16-byte load per slot.
+  // fp32 inputs (the combine's per-slot rows) take 4 outputs per thread below
+  // 2^22 outputs: a decode batch (M = 64, N = 4096) then spans every CU
+  // (measured 8.1 -> 6.2 us on the C2 combine); larger ones take 8 (the C5
+  // combine, 4096 x 4096: 111.9 -> 103.5 us). bf16 inputs keep one 16-byte
+  // load per slot.
   if constexpr (std::is_same<Tin, float>::value) {
-    if (H % 4 == 0 && aligned)
+    if (H % 4 == 0 && aligned && !(H % 8 == 0 && M * H >= (int64_t(1) << 22)))
       return launch_vec<Tin, Tout, 4>(y, M, top_k, H, rw, scale, out, nparts, pstride, stream);
   }
   if (H % 8 == 0 && aligned)
