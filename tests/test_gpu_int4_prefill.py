@@ -102,6 +102,8 @@ CASES = [  # M, E, N, K, top_k, routing
     (2048, 48, 1024, 2048, 8, "zipf"),  # more tiles than workgroups
     (16, 8, 1024, 2048, 2, "uniform"),  # C1 shape, forced onto the tile kernel
     (sum(CLASS_ROWS), len(CLASS_ROWS), 512, 512, 1, "classes"),  # every tile height and order class
+    (600, 1, 256, 512, 1, "uniform"),   # one expert: three row blocks, the last a tail
+    (512, 1024, 256, 256, 4, "zipf"),   # the most experts the tile kernel takes, most of them empty
 ]
 
 
