@@ -134,10 +134,14 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& p) {
   auto xcd_tiles = [&](int x) { return B > x ? (B - x + kXcds - 1) / kXcds * NB : 0; };
   auto xcd_tile = [&](int x, int n) { return (x + kXcds * (n / NB)) * NB + n % NB; };
 
-  // A staging: thread -> (row st_row + kStRows i, 16-byte chunk st_kv). The two
-  // 16-lane halves of each 32-lane LDS write group take rows 8 apart, whose
-  // bank groups are disjoint.
-  const int st_kv = tid & 15, st_g = tid >> 4;
+  // A staging: thread -> (row st_row + kStRows i, global 16-byte chunk st_kv).
+  // Global chunk kv lands at LDS chunk (kv & 3) * 4 + (kv >> 2) (an involution),
+  // so lane l of a row loads chunk (l & 3) * 4 + (l >> 2) and the row's 16 lanes
+  // write consecutive LDS chunks: the lane-order transpose of the reverse
+  // assignment (lane l loads chunk l) cost 62.6 M bank-conflict cycles per C5
+  // launch, this one none. The two 16-lane halves of each 32-lane LDS write
+  // group take rows 8 apart.
+  const int st_kv = ((tid & 3) << 2) | ((tid >> 2) & 3), st_g = tid >> 4;
   const int st_row = (st_g & 1) * 8 + ((st_g >> 1) & 7) + 16 * (st_g >> 4);
 
   // Tile order. With a queue, each workgroup takes the next tile of its XCD's
