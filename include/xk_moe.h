@@ -170,7 +170,9 @@ int xk_moe_int4_w4a16_noalloc(const void* A, int32_t a_dtype, int64_t M, int64_t
 int32_t xk_moe_int4_block_size(int64_t M, int64_t top_k, int64_t E);
 /* Which grouped-GEMM kernel a fused call with these shapes runs: 0 the scalar
  * kernel (shapes the MFMA kernels do not take, including activations or one
- * expert's packed weights of 2^31 bytes or more), 1 the decode weight-streaming
+ * expert's packed weights of 2^31 bytes or more; the fused call runs a batch
+ * whose activations reach 2^31 bytes as token chunks, each with the choice for
+ * its own M), 1 the decode weight-streaming
  * kernel, 2 the prefill MFMA tile kernel. num_global_experts: the expert map's
  * size for an expert-parallel call with a workspace of
  * xk_moe_int4_w4a16_ep_workspace_bytes, else 0. No counterpart in the

@@ -174,3 +174,24 @@ def test_default_choice_uses_tile_kernel_at_prefill_sizes(dev):
     default = _slot_rows(A, packed, scale, ids, 0)
     tile = _slot_rows(A, packed, scale, ids, _lib._XK_INT4_TEST_FORCE_TILE)
     assert torch.equal(default, tile)
+
+
+def test_batch_past_buffer_reach_runs_in_token_chunks(dev):
+    """150,000 tokens at K = 7168: 2.15 GB of activations, past what the MFMA
+    kernels address through 32-bit buffer offsets (one launch would take the
+    scalar kernel). The fused call runs token chunks on the MFMA kernels, and a
+    token's output depends only on its own slots, so it equals two calls over
+    another split of the batch bit for bit."""
+    M, E, N, K, k = 150_000, 4, 256, 7168, 1
+    print(f"token chunks M={M} E={E} N={N} K={K}", flush=True)
+    kern = lambda m: _lib.query("xk_moe_int4_kernel", m, k, E, N, K, _lib.XK_DT_BF16, 32, 0, 0)
+    assert kern(M) == 0 and kern(M // 2) == 2
+    ids = uniform_topk(M, k, E, 41)
+    A, packed, scale, ids, w = _inputs(M, E, N, K, ids, seed=43)
+    whole = _fused(A, packed, scale, ids, w, 0)
+    cut = 100_000
+    parts = torch.cat([_fused(A[:cut], packed, scale, ids[:cut], w[:cut], 0),
+                       _fused(A[cut:], packed, scale, ids[cut:], w[cut:], 0)])
+    torch.cuda.synchronize()
+    assert torch.isfinite(whole.float()).all()
+    assert torch.equal(whole, parts)

@@ -285,6 +285,31 @@ int xk_moe_int4_w4a16(const void* A, int32_t a_dtype, int64_t M, int64_t K,
   if (workspace == nullptr || workspace_bytes < need)
     return set_error(XK_ERR_WORKSPACE, "int4: workspace %lld B < %lld B",
                      (long long)workspace_bytes, (long long)need);
+  // A batch whose activations the MFMA kernels cannot address (2^31 bytes
+  // through buffer offsets) runs as consecutive token chunks of the largest
+  // size they take: a token's output depends only on its own slots (each slot
+  // row is a fixed-order K sum, the combine sums a token's slots in slot
+  // order), so the chunks write what one call would, bit for bit, with the
+  // MFMA kernels instead of the scalar one. Each chunk lays out its smaller
+  // workspace at the start of this one; the stream orders them.
+  if (flags == 0 && int4_kernel_code(M, top_k, E, N, K, a_dtype, group_size, 0, 0) == 0) {
+    const int64_t elem = a_dtype == XK_DT_FP32 ? 4 : 2;
+    int64_t mc = ((int64_t(1) << 31) - 1) / (K * elem);
+    while (mc > 0 && int4_kernel_code(mc, top_k, E, N, K, a_dtype, group_size, 0, 0) == 0) mc /= 2;
+    if (mc > 0 && mc < M) {
+      for (int64_t m0 = 0; m0 < M; m0 += mc) {
+        const int64_t mm = std::min(mc, M - m0);
+        if (int rc = xk_moe_int4_w4a16(static_cast<const char*>(A) + m0 * K * elem, a_dtype, mm, K,
+                                       packed, scale, E, N, group_size, topk_ids + m0 * top_k,
+                                       topk_w != nullptr ? topk_w + m0 * top_k : nullptr, top_k,
+                                       expert_map, num_global_experts, mul_routed_weight, flags,
+                                       static_cast<char*>(out) + m0 * N * elem, workspace,
+                                       workspace_bytes, stream))
+          return rc;
+      }
+      return XK_OK;
+    }
+  }
   const int64_t numel = M * top_k;
   AlignScratch al(numel, int(E), int4_block_size());
   const int64_t planes_at = int4_planes_offset(M, top_k, E, K);
