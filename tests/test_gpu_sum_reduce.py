@@ -20,7 +20,8 @@ TOL = {torch.bfloat16: (1.6e-2, 1e-2), torch.float32: (1e-5, 1e-4)}
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("M,top_k,H", [(128, 8, 7168), (1, 8, 7168), (37, 4, 96), (5, 3, 7),
-                                       (9, 1, 64), (3, 9, 40), (16, 6, 4096), (4, 2, 12)])
+                                       (9, 1, 64), (3, 9, 40), (16, 6, 4096), (4, 2, 12),
+                                       (640, 2, 7168)])  # 2^22 outputs or more: fp32 8-wide path
 @pytest.mark.parametrize("wkind", ["fp32", "bf16", "none"])
 def test_matches_oracle(dtype, M, top_k, H, wkind, dev):
     g = torch.Generator().manual_seed(M * 31 + H)
